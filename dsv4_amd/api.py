@@ -1,0 +1,293 @@
+"""Drop-in for ``sparse_attn_sharedkv_tilelang/api.py``: ``sparse_attn_sharedkv``.
+
+Same signature, argument meaning, scenario routing and return convention as
+api.py:129-397; the computation runs in libsas's gfx950 HIP kernels.
+
+Scenario (api.py:196-202): ``cmp_kv is None`` -> SWA (window only);
+``cmp_sparse_indices is None`` -> CFA (window + every compressed row below
+the causal threshold); otherwise SCFA (window + top-k compressed rows).
+
+Relaxations of the reference's shape guard (api.py:279-282), which are not
+signature changes: the query head count may be any multiple of 16; the
+head dim may be 512 or 576 (576 = 512 latent + 64 rope; the output and V are
+the first 512 channels, so ``out`` is ``[..., 512]``); any top-k width; any
+block size; and an fp8 cache given as uint8 ``[num_blocks, block_size, 1,
+656]`` rows (see :mod:`dsv4_amd.paged`) with a bf16 query.
+
+``metadata`` is validated (int32, 1024 entries) and synthesised with the
+bit-exact scheduler when omitted (api.py:335-366). The GPU kernel does not
+need it for scheduling: it launches one workgroup per (token, head group,
+KV split) and covers every valid token by construction.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _lib
+from .metadata import SAS_META_SIZE, sparse_attn_sharedkv_metadata
+
+DEFAULT_CORE_NUM = 24
+_DT = {torch.bfloat16: _lib.SAS_DT_BF16, torch.float16: _lib.SAS_DT_FP16}
+FP8_ROW_BYTES = 656
+
+
+def _dev_i32(t: torch.Tensor, device) -> torch.Tensor:
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+class PreparedCall:
+    """Arguments of one forward, resolved and allocated; :meth:`launch` runs
+    the kernels on the current (or given) stream without host syncs."""
+
+    def __init__(self, args: _lib.SasFwdArgs, keep: list, out, lse, layout_q, B, S_max):
+        self.args = args
+        self._keep = keep
+        self.out = out
+        self.lse = lse
+        self.layout_q = layout_q
+        self.B = B
+        self.S_max = S_max
+        ns = C.c_int32(0)
+        ws = C.c_size_t(0)
+        _lib.check(_lib.lib().sas_fwd_plan(C.byref(args), C.byref(ns), C.byref(ws)),
+                   "sparse_attn_sharedkv")
+        self.num_splits = ns.value
+        self.workspace = None
+        if ws.value:
+            self.workspace = torch.empty(ws.value, dtype=torch.uint8, device=out.device)
+            args.workspace = self.workspace.data_ptr()
+            args.workspace_bytes = ws.value
+        args.num_splits = self.num_splits
+
+    def launch(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+        st = stream if stream is not None else torch.cuda.current_stream(self.out.device)
+        _lib.check(_lib.lib().sas_fwd_v1(C.byref(self.args), C.c_void_p(st.cuda_stream)),
+                   "sparse_attn_sharedkv")
+
+    def result(self, return_softmax_lse: bool):
+        out, lse = self.out, self.lse
+        if self.layout_q == "BSND":
+            out = out.reshape(self.B, self.S_max, out.shape[1], out.shape[2])
+            lse = lse.reshape(self.B, self.S_max, lse.shape[1])
+        return (out, lse) if return_softmax_lse else out
+
+
+def prepare_sparse_attn_sharedkv(
+    q: torch.Tensor,
+    *,
+    ori_kv: torch.Tensor,
+    cmp_kv: Optional[torch.Tensor] = None,
+    cmp_sparse_indices: Optional[torch.Tensor] = None,
+    ori_block_table: torch.Tensor,
+    cmp_block_table: Optional[torch.Tensor] = None,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    seqused_q: Optional[torch.Tensor] = None,
+    seqused_kv: torch.Tensor,
+    sinks: torch.Tensor,
+    metadata: Optional[torch.Tensor] = None,
+    softmax_scale: float,
+    cmp_ratio: Optional[int] = None,
+    ori_mask_mode: int = 4,
+    cmp_mask_mode: int = 3,
+    ori_win_left: int = 127,
+    ori_win_right: int = 0,
+    layout_q: str = "TND",
+    layout_kv: str = "PA_ND",
+    core_num: int = DEFAULT_CORE_NUM,
+    topk_cmp: Optional[int] = None,
+    num_splits: int = 0,
+) -> PreparedCall:
+    """Validate and resolve the arguments of :func:`sparse_attn_sharedkv`
+    (api.py:186-366) and allocate outputs; see that function."""
+    del seqused_q  # API-parity placeholder, as in the reference (api.py:186)
+    assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
+    assert cmp_mask_mode == 3 or cmp_kv is None, "only cmp_mask_mode=3 supported"
+    assert ori_win_right == 0, "only ori_win_right=0 supported"
+    assert layout_kv == "PA_ND", "only layout_kv=PA_ND supported"
+    assert layout_q in ("TND", "BSND"), f"unsupported layout_q={layout_q!r}"
+    if q.dtype not in _DT:
+        raise ValueError(f"unsupported torch dtype {q.dtype}")
+    if not q.is_cuda:
+        raise ValueError("sparse_attn_sharedkv runs on the GPU: q must be a device tensor")
+    dev = q.device
+
+    scenario = _lib.SAS_SWA if cmp_kv is None else (
+        _lib.SAS_CFA if cmp_sparse_indices is None else _lib.SAS_SCFA)
+
+    # ---- flat [total_tokens, N1, D] view + per-batch token offsets ----------
+    if layout_q == "TND":
+        assert cu_seqlens_q is not None, "cu_seqlens_q is required for TND"
+        cu = cu_seqlens_q.to(torch.int32).cpu()
+        B = cu.numel() - 1
+        seq_lens = (cu[1:] - cu[:-1]).tolist()
+        S_max = max(seq_lens) if seq_lens else 0
+        T1, N1, D = q.shape
+        q_flat = q
+        q_prefix = cu[:-1]
+        act_q = torch.tensor(seq_lens, dtype=torch.int32)
+        idx_flat = cmp_sparse_indices if scenario == _lib.SAS_SCFA else None
+    else:
+        B, S_max, N1, D = q.shape
+        T1 = B * S_max
+        q_flat = q.reshape(T1, N1, D)
+        q_prefix = torch.arange(B, dtype=torch.int32) * S_max
+        seq_lens = [S_max] * B
+        if cu_seqlens_q is not None:
+            cu = cu_seqlens_q.to(torch.int32).cpu()
+            seq_lens = (cu[1:] - cu[:-1]).tolist()
+        act_q = torch.tensor(seq_lens, dtype=torch.int32)
+        idx_flat = None
+        if scenario == _lib.SAS_SCFA:
+            ci = cmp_sparse_indices
+            idx_flat = ci.reshape(T1, ci.shape[2], ci.shape[3])
+    if B < 1:
+        raise ValueError("batch must be at least 1")
+
+    # ---- top-k / scenario tensors (api.py:244-277) ---------------------------
+    fp8 = ori_kv.dtype == torch.uint8
+    if scenario == _lib.SAS_SCFA:
+        N2 = idx_flat.shape[1]
+        K = topk_cmp if topk_cmp is not None else idx_flat.shape[2]
+        assert K == idx_flat.shape[2], "topk_cmp does not match cmp_sparse_indices last dim"
+        if idx_flat.shape[0] != T1:
+            raise ValueError(f"cmp_sparse_indices has {idx_flat.shape[0]} rows, q has {T1} tokens")
+    elif scenario == _lib.SAS_CFA:
+        N2 = cmp_kv.shape[2]
+        if cmp_ratio is None:
+            cmp_ratio = 4
+        K = int(seqused_kv.max().item()) // cmp_ratio if seqused_kv.numel() else 0
+    else:
+        N2 = ori_kv.shape[2]
+        K = 0
+    row = ori_kv.shape[-1]
+    if N2 != 1 or N1 % 16 != 0 or D not in (512, 576) or (fp8 and (D != 576 or row != FP8_ROW_BYTES)):
+        raise ValueError(
+            f"supported: N1 a multiple of 16, N2=1, D in (512, 576), fp8 rows of "
+            f"{FP8_ROW_BYTES} bytes with D=576 (got N1={N1}, N2={N2}, D={D}, kv row={row})")
+    if fp8 and q.dtype != torch.bfloat16:
+        raise ValueError("fp8 caches need a bfloat16 query")
+    if not fp8 and (ori_kv.dtype != q.dtype or row != D):
+        raise ValueError(f"ori_kv must be {q.dtype} rows of {D} (got {ori_kv.dtype}, {row})")
+    if cmp_kv is not None and (cmp_kv.dtype != ori_kv.dtype or cmp_kv.shape[-1] != row):
+        raise ValueError("cmp_kv must use the same row format as ori_kv")
+    cmp_ratio_eff = cmp_ratio if cmp_ratio is not None else 4
+    if scenario >= _lib.SAS_CFA and cmp_ratio_eff < 1:
+        raise ValueError("cmp_ratio must be >= 1")
+
+    # ---- metadata (api.py:335-366): synthesised when absent, validated ------
+    if metadata is None:
+        meta_kwargs = dict(
+            num_heads_q=N1, num_heads_kv=N2, head_dim=D,
+            cu_seqlens_q=cu_seqlens_q if layout_q == "TND" else None,
+            seqused_kv=seqused_kv, batch_size=int(B), max_seqlen_q=int(S_max),
+            max_seqlen_kv=int(seqused_kv.max().item()) if seqused_kv.numel() else 0,
+            ori_mask_mode=ori_mask_mode, ori_win_left=ori_win_left, ori_win_right=ori_win_right,
+            layout_q=layout_q, layout_kv=layout_kv, has_ori_kv=True,
+            has_cmp_kv=cmp_kv is not None, aic_core_num=core_num)
+        if scenario >= _lib.SAS_CFA:
+            meta_kwargs["cmp_ratio"] = cmp_ratio_eff
+            meta_kwargs["cmp_mask_mode"] = cmp_mask_mode
+        if scenario == _lib.SAS_SCFA:
+            meta_kwargs["cmp_topk"] = K
+        metadata = sparse_attn_sharedkv_metadata(**meta_kwargs)
+    assert metadata.numel() == SAS_META_SIZE, (
+        f"metadata must have {SAS_META_SIZE} int32 entries (got {metadata.numel()})")
+
+    # ---- device operands ------------------------------------------------------
+    keep = []
+
+    def d(t, dtype=None):
+        if t is None:
+            return None
+        t = t.to(device=dev, dtype=dtype) if dtype is not None else t.to(device=dev)
+        t = t.contiguous()
+        keep.append(t)
+        return t
+
+    qd = d(q_flat)
+    okv = d(ori_kv)
+    obt = d(ori_block_table, torch.int32)
+    ckv = d(cmp_kv) if scenario >= _lib.SAS_CFA else None
+    cbt = d(cmp_block_table, torch.int32) if scenario >= _lib.SAS_CFA else None
+    cidx = d(idx_flat, torch.int32) if scenario == _lib.SAS_SCFA else None
+    host = torch.cat([q_prefix.to(torch.int32), act_q,
+                      seqused_kv.to(device="cpu", dtype=torch.int32).reshape(-1)])
+    if seqused_kv.numel() != B:
+        raise ValueError(f"seqused_kv has {seqused_kv.numel()} entries, batch is {B}")
+    hd = d(host)
+    snk = d(sinks, torch.float32)
+    if snk.numel() != N1:
+        raise ValueError(f"sinks must have {N1} entries (got {snk.numel()})")
+    out = torch.empty((T1, N1, 512), dtype=q.dtype, device=dev)
+    lse = torch.empty((T1, N1), dtype=torch.float32, device=dev)
+
+    a = _lib.SasFwdArgs()
+    a.q, a.ori_kv, a.ori_block_table = qd.data_ptr(), okv.data_ptr(), obt.data_ptr()
+    a.cmp_kv = ckv.data_ptr() if ckv is not None else None
+    a.cmp_block_table = cbt.data_ptr() if cbt is not None else None
+    a.cmp_indices = cidx.data_ptr() if cidx is not None else None
+    a.q_prefix = hd.data_ptr()
+    a.act_q = hd.data_ptr() + 4 * B
+    a.act_kv = hd.data_ptr() + 8 * B
+    a.sinks, a.out, a.lse = snk.data_ptr(), out.data_ptr(), lse.data_ptr()
+    a.T, a.B, a.H, a.D, a.DV = T1, B, N1, D, 512
+    a.ori_block_size, a.ori_bt_stride, a.ori_num_blocks = okv.shape[1], obt.shape[1], okv.shape[0]
+    if ckv is not None:
+        a.cmp_block_size, a.cmp_bt_stride, a.cmp_num_blocks = ckv.shape[1], cbt.shape[1], ckv.shape[0]
+    a.K = int(K)
+    a.scenario = scenario
+    a.q_dtype = _DT[q.dtype]
+    a.kv_dtype = _lib.SAS_DT_FP8_E4M3_ROW656 if fp8 else _DT[q.dtype]
+    a.cmp_ratio = int(cmp_ratio_eff)
+    a.win_left = int(ori_win_left)
+    a.softmax_scale = float(softmax_scale)
+    a.num_splits = int(num_splits)
+    return PreparedCall(a, keep, out, lse, layout_q, B, S_max)
+
+
+def sparse_attn_sharedkv(
+    q: torch.Tensor,
+    *,
+    ori_kv: torch.Tensor,
+    cmp_kv: Optional[torch.Tensor] = None,
+    cmp_sparse_indices: Optional[torch.Tensor] = None,
+    ori_block_table: torch.Tensor,
+    cmp_block_table: Optional[torch.Tensor] = None,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    seqused_q: Optional[torch.Tensor] = None,
+    seqused_kv: torch.Tensor,
+    sinks: torch.Tensor,
+    metadata: Optional[torch.Tensor] = None,
+    softmax_scale: float,
+    cmp_ratio: Optional[int] = None,
+    ori_mask_mode: int = 4,
+    cmp_mask_mode: int = 3,
+    ori_win_left: int = 127,
+    ori_win_right: int = 0,
+    layout_q: str = "TND",
+    layout_kv: str = "PA_ND",
+    return_softmax_lse: bool = False,
+    core_num: int = DEFAULT_CORE_NUM,
+    topk_cmp: Optional[int] = None,
+) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """Forward pass; returns ``attention_out`` in ``q``'s layout, or
+    ``(attention_out, lse)`` when ``return_softmax_lse`` (api.py:129-397).
+
+    ``attention_out`` is ``[T1, N1, 512]`` (TND) or ``[B, S1, N1, 512]``
+    (BSND) in q's dtype; ``lse`` is fp32 ``[T1, N1]`` / ``[B, S1, N1]`` with
+    ``lse = max + ln(sum)`` over all attended keys and the sink.
+    """
+    call = prepare_sparse_attn_sharedkv(
+        q, ori_kv=ori_kv, cmp_kv=cmp_kv, cmp_sparse_indices=cmp_sparse_indices,
+        ori_block_table=ori_block_table, cmp_block_table=cmp_block_table,
+        cu_seqlens_q=cu_seqlens_q, seqused_q=seqused_q, seqused_kv=seqused_kv, sinks=sinks,
+        metadata=metadata, softmax_scale=softmax_scale, cmp_ratio=cmp_ratio,
+        ori_mask_mode=ori_mask_mode, cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
+        ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
+        core_num=core_num, topk_cmp=topk_cmp)
+    call.launch()
+    return call.result(return_softmax_lse)

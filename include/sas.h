@@ -1,0 +1,161 @@
+/*
+ * sas.h — C ABI of libsas.so, the MI355X (gfx950) implementation of
+ * sparse_attn_sharedkv: fused sliding-window + top-k compressed-KV attention
+ * over one shared K=V latent cache, with online softmax and per-head sinks.
+ *
+ * Plain pointers and sizes only. Device pointers are HIP device addresses;
+ * `stream` is a hipStream_t passed as void*. Functions return SAS_OK (0) or
+ * an error code, with a message available from sas_last_error() (thread-local).
+ * The library never allocates or frees caller memory and keeps no pointer
+ * after a call returns.
+ */
+#ifndef SAS_H_
+#define SAS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Metadata layout, sparse_attn_sharedkv_tilelang/metadata.py:38-60. */
+#define SAS_META_SIZE 1024
+#define SAS_AIC_CORE_NUM 36
+#define SAS_AIV_CORE_NUM 72
+#define SAS_FA_METADATA_SIZE 8
+#define SAS_FD_METADATA_SIZE 8
+
+enum {
+  SAS_OK = 0,
+  SAS_EINVAL = 1,  /* bad argument / unsupported shape */
+  SAS_ELAUNCH = 2, /* HIP launch or runtime error */
+  SAS_ENOWS = 3    /* workspace missing or too small */
+};
+
+/* Element formats. */
+enum {
+  SAS_DT_BF16 = 0,
+  SAS_DT_FP16 = 1,
+  /* 656-byte fp8 cache row: 512 e4m3fn latent | 4 fp32 scales (one per 128
+     latent channels) | 64 bf16 rope channels. Dequantised value =
+     e4m3(byte) * scale[channel / 128]. */
+  SAS_DT_FP8_E4M3_ROW656 = 2
+};
+
+/* Index-source scenario, sparse_attn_sharedkv_tilelang/api.py:196-202. */
+enum { SAS_SWA = 1, SAS_CFA = 2, SAS_SCFA = 3 };
+
+/*
+ * Scheduler inputs; mirrors the keyword arguments of
+ * sparse_attn_sharedkv_metadata (sparse_attn_sharedkv_tilelang/metadata.py:
+ * 1018-1045). Optional int32 arrays are (pointer, element count) pairs with
+ * a NULL pointer / zero count when absent. Layouts are the reference strings
+ * ("BSND", "BSH", "TND", "BNSD", "PA_ND", ...).
+ */
+typedef struct SasMetaParams {
+  int64_t num_heads_q, num_heads_kv, head_dim;
+  int64_t batch_size, max_seqlen_q, max_seqlen_kv;
+  int64_t ori_topk, cmp_topk, cmp_ratio;
+  int64_t ori_mask_mode, cmp_mask_mode, ori_win_left, ori_win_right;
+  const char* layout_q;
+  const char* layout_kv;
+  int32_t has_ori_kv, has_cmp_kv;
+  int64_t aic_core_num, aiv_core_num;
+  const int32_t* cu_seqlens_q;      int64_t n_cu_seqlens_q;
+  const int32_t* cu_seqlens_ori_kv; int64_t n_cu_seqlens_ori_kv;
+  const int32_t* cu_seqlens_cmp_kv; int64_t n_cu_seqlens_cmp_kv;
+  const int32_t* seqused_q;         int64_t n_seqused_q;
+  const int32_t* seqused_kv;        int64_t n_seqused_kv;
+} SasMetaParams;
+
+/*
+ * Host-side cost-balanced schedule, bit-exact with the reference scheduler.
+ * Replaces sparse_attn_sharedkv_tilelang/metadata.py:1018-1086
+ * (_MetadataScheduler.run, metadata.py:258-1015). Writes int32[1024]:
+ * fa[36][8] (enable, bn2_start, m_start, s2_start, bn2_end, m_end, s2_end,
+ * first_fd_ws) followed by fd[72][8] and zero padding.
+ */
+int sas_metadata_v1(const SasMetaParams* p, int32_t* out /* [SAS_META_SIZE] */);
+
+/*
+ * Forward arguments; the device tensors of the reference kernel callable
+ * (sparse_attn_sharedkv_tilelang/kernel.py:158-178) plus dims and strides.
+ * q/out are flat token-major [T, H, D] / [T, H, DV]; q_prefix/act_q give each
+ * batch's first packed token and query length (TND: cu_seqlens_q[:-1] and
+ * lengths; BSND: b*S_max and S_max). Caches are [num_blocks, block_size, 1,
+ * row] with row = D elements (bf16/fp16) or 656 bytes (fp8 rows).
+ */
+typedef struct SasFwdArgs {
+  const void* q;                 /* [T, H, D] q_dtype */
+  const void* ori_kv;            /* paged raw KV */
+  const int32_t* ori_block_table;/* [B, ori_bt_stride] */
+  const void* cmp_kv;            /* paged compressed KV (CFA/SCFA) or NULL */
+  const int32_t* cmp_block_table;/* [B, cmp_bt_stride] or NULL */
+  const int32_t* cmp_indices;    /* [T, 1, K] (SCFA) or NULL */
+  const int32_t* q_prefix;       /* [B] */
+  const int32_t* act_q;          /* [B] */
+  const int32_t* act_kv;         /* [B] seqused_kv */
+  const float* sinks;            /* [H] */
+  void* out;                     /* [T, H, DV] q_dtype */
+  float* lse;                    /* [T, H] */
+  void* workspace;               /* split-KV partials, see sas_fwd_workspace_size */
+  size_t workspace_bytes;
+  int64_t T, B, H, D, DV;
+  int64_t ori_block_size, ori_bt_stride, ori_num_blocks;
+  int64_t cmp_block_size, cmp_bt_stride, cmp_num_blocks;
+  int64_t K;                     /* SCFA: top-k width; CFA: compressed slots per row */
+  int32_t scenario;              /* SAS_SWA / SAS_CFA / SAS_SCFA */
+  int32_t q_dtype;               /* SAS_DT_BF16 or SAS_DT_FP16 */
+  int32_t kv_dtype;              /* q_dtype, or SAS_DT_FP8_E4M3_ROW656 with bf16 q */
+  int32_t cmp_ratio;
+  int32_t win_left;              /* ori_win_left (window = win_left + 1 rows) */
+  float softmax_scale;
+  int32_t num_splits;            /* KV splits per token; 0 = choose automatically */
+} SasFwdArgs;
+
+/*
+ * Split count the library would use (after auto-selection) and the
+ * workspace bytes it needs for these arguments (0 when no split is used).
+ */
+int sas_fwd_plan(const SasFwdArgs* a, int32_t* num_splits, size_t* workspace_bytes);
+
+/*
+ * Launch the fused forward on `stream`: one workgroup per (token, head group,
+ * KV split), gather through block tables into LDS, bf16/fp16 MFMA for QK^T and
+ * PV, sink-seeded online softmax, and (when splits > 1) the LSE combine.
+ * Replaces the jitted callable of kernel.py:156-178 / api.py:372-384.
+ */
+int sas_fwd_v1(const SasFwdArgs* a, void* stream);
+
+/*
+ * Split-KV LSE combine (no counterpart launched by the reference: its
+ * flash-decode fields stay zero, metadata.py:323-325): for each (token, head)
+ * M = max(sink, m_i), L = e^(sink-M) + sum_i l_i e^(m_i-M),
+ * out = sum_i e^(m_i-M) O_i / L, lse = M + ln L.
+ * part_o [T, S, H, DV] fp32 (unnormalised), part_ml [T, S, H, 2] fp32
+ * (running max in log2 units, running sum).
+ */
+typedef struct SasCombineArgs {
+  const float* part_o;
+  const float* part_ml;
+  const float* sinks;
+  void* out;
+  float* lse;
+  int64_t T, S, H, DV;
+  int32_t out_dtype;             /* SAS_DT_BF16 or SAS_DT_FP16 */
+} SasCombineArgs;
+
+int sas_combine_v1(const SasCombineArgs* a, void* stream);
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char* sas_last_error(void);
+
+/* Library version string. */
+const char* sas_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAS_H_ */

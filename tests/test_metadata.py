@@ -1,0 +1,180 @@
+"""Scheduler parity (CPU): libsas's C++ scheduler and the oracle restatement
+against the reference's recorded outputs, against each other on fuzzed
+inputs, and the reference suite's invariants
+(test_sparse_attn_sharedkv.py:721-924)."""
+
+from __future__ import annotations
+
+import json
+import os
+import random
+
+import pytest
+import torch
+
+from dsv4_amd import cases as C
+from dsv4_amd.metadata import (AIC_CORE_NUM, FA_METADATA_SIZE, SAS_META_SIZE,
+                               sparse_attn_sharedkv_metadata)
+from oracle.metadata_ref import metadata_ref
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+with open(os.path.join(HERE, "golden", "metadata_fixtures.json")) as f:
+    FIX = json.load(f)
+TENSOR_KEYS = ("cu_seqlens_q", "cu_seqlens_ori_kv", "cu_seqlens_cmp_kv", "seqused_q", "seqused_kv")
+
+
+def _kw(kw):
+    out = dict(kw)
+    for k in TENSOR_KEYS:
+        if out.get(k) is not None:
+            out[k] = torch.tensor(out[k], dtype=torch.int32)
+    return out
+
+
+def _expected(case):
+    exp = [0] * SAS_META_SIZE
+    for i, v in case["nonzero"]:
+        exp[i] = v
+    return exp
+
+
+@pytest.mark.parametrize("case", FIX["cases"], ids=[c["name"] for c in FIX["cases"]])
+def test_cpp_scheduler_matches_reference_vectors(case):
+    got = sparse_attn_sharedkv_metadata(**_kw(case["kwargs"]))
+    assert got.dtype == torch.int32 and got.shape == (SAS_META_SIZE,)
+    assert got.tolist() == _expected(case)
+
+
+@pytest.mark.parametrize("case", FIX["cases"], ids=[c["name"] for c in FIX["cases"]])
+def test_oracle_scheduler_matches_reference_vectors(case):
+    assert metadata_ref(**_kw(case["kwargs"])) == _expected(case)
+
+
+def test_design_note_worked_example():
+    """B=2, S1=[4,2], S2=[1500,500], aic=3, SCFA r=128 k=512: FA rows
+    (1,0,0,0,0,2,0), (1,0,2,0,1,0,0), (1,1,0,0,2,0,0); FD section zero
+    (SparseAttnSharedkvMetadata详解.md:1819-1833)."""
+    md = sparse_attn_sharedkv_metadata(
+        num_heads_q=64, num_heads_kv=1, head_dim=512,
+        cu_seqlens_q=torch.tensor([0, 4, 6], dtype=torch.int32),
+        seqused_kv=torch.tensor([1500, 500], dtype=torch.int32), batch_size=2,
+        max_seqlen_q=4, max_seqlen_kv=1500, cmp_topk=512, cmp_ratio=128, layout_q="TND",
+        aic_core_num=3, aiv_core_num=6).tolist()
+    assert md[0:7] == [1, 0, 0, 0, 0, 2, 0]
+    assert md[8:15] == [1, 0, 2, 0, 1, 0, 0]
+    assert md[16:23] == [1, 1, 0, 0, 2, 0, 0]
+    assert not any(md[24:])
+
+
+def _fuzz_kwargs(rnd: random.Random):
+    B = rnd.choice([1, 2, 4, 7, 16, 48])
+    layout = rnd.choice(["TND", "BSND", "BNSD"])
+    n2 = rnd.choice([1, 1, 2, 4])
+    g = rnd.choice([1, 16, 64, 128])
+    ql = [rnd.choice([0, 1, 2, 3, 5, 64, 65, 200]) for _ in range(B)]
+    kl = [max(0, q + rnd.choice([0, 1, 7, 511, 512, 513, 4000])) for q in ql]
+    kw = dict(num_heads_q=g * n2, num_heads_kv=n2, head_dim=576, batch_size=B,
+              max_seqlen_q=max(ql), max_seqlen_kv=max(kl), layout_q=layout,
+              has_cmp_kv=rnd.random() < 0.7, aic_core_num=rnd.choice([1, 2, 5, 24, 36]),
+              ori_win_left=rnd.choice([127, 0, 1, 511, 512, -1]),
+              ori_mask_mode=rnd.choice([4, 4, 3, 0, 1, 2]))
+    if rnd.random() < 0.8:
+        kw["seqused_kv"] = torch.tensor(kl, dtype=torch.int32)
+    if layout == "TND":
+        cu = [0]
+        for x in ql:
+            cu.append(cu[-1] + x)
+        kw["cu_seqlens_q"] = torch.tensor(cu, dtype=torch.int32)
+    elif rnd.random() < 0.5:
+        kw["seqused_q"] = torch.tensor(ql, dtype=torch.int32)
+    if kw["has_cmp_kv"]:
+        kw["cmp_ratio"] = rnd.choice([1, 4, 128])
+        kw["cmp_topk"] = rnd.choice([0, 64, 512, 2048])
+    return kw
+
+
+def test_cpp_scheduler_matches_oracle_fuzz():
+    rnd = random.Random(20260)
+    for i in range(300):
+        kw = _fuzz_kwargs(rnd)
+        got = sparse_attn_sharedkv_metadata(**kw).tolist()
+        assert got == metadata_ref(**kw), f"fuzz case {i}: {kw}"
+
+
+def _meta_for(cfg: C.Config, aic=24):
+    ql, kl = C.seq_lengths(cfg)
+    cu = [0]
+    for x in ql:
+        cu.append(cu[-1] + x)
+    kw = dict(num_heads_q=cfg.H, num_heads_kv=1, head_dim=cfg.D,
+              cu_seqlens_q=torch.tensor(cu, dtype=torch.int32),
+              seqused_kv=torch.tensor(kl, dtype=torch.int32), batch_size=cfg.B,
+              max_seqlen_q=max(ql), max_seqlen_kv=max(kl), layout_q="TND",
+              has_cmp_kv=cfg.scenario >= 2, aic_core_num=aic)
+    if cfg.scenario >= 2:
+        kw["cmp_ratio"] = cfg.cmp_ratio
+    if cfg.scenario == 3:
+        kw["cmp_topk"] = cfg.K
+    return sparse_attn_sharedkv_metadata(**kw), ql
+
+
+ALL_CFGS = list(C.REF_SCENARIOS.values()) + list(C.CONFIGS.values())
+
+
+@pytest.mark.parametrize("cfg", ALL_CFGS, ids=[c.name for c in ALL_CFGS])
+def test_continuity(cfg):
+    """Enabled cores chain: (start) of core i == (end) of core i-1
+    (test_sparse_attn_sharedkv.py:721-792)."""
+    md, _ = _meta_for(cfg)
+    fa = md[: AIC_CORE_NUM * FA_METADATA_SIZE].view(AIC_CORE_NUM, FA_METADATA_SIZE)
+    used = fa[fa[:, 0] == 1].tolist()
+    assert used
+    prev = (0, 0, 0)
+    for _, bs, ms, ss, be, me, se, _ in used:
+        assert (bs, ms, ss) == prev
+        prev = (be, me, se)
+    assert prev[0] in (cfg.B, 0)
+
+
+@pytest.mark.parametrize("cfg", ALL_CFGS, ids=[c.name for c in ALL_CFGS])
+def test_kernel_walk_covers_every_token_once(cfg):
+    """Walking each core's linearised (bn2, m) window as the reference kernel
+    does (kernel.py:254-277) visits every valid (b, s) exactly once
+    (test_sparse_attn_sharedkv.py:795-893)."""
+    md, ql = _meta_for(cfg)
+    fa = md[: AIC_CORE_NUM * FA_METADATA_SIZE].view(AIC_CORE_NUM, FA_METADATA_SIZE).tolist()
+    max_seq = max(ql)
+    seen = []
+    for en, bs, ms, _, be, me, _, _ in fa:
+        if not en:
+            continue
+        for pid in range(bs * max_seq + ms, be * max_seq + me):
+            b, s = divmod(pid, max_seq)
+            if b < cfg.B and s < ql[b]:
+                seen.append((b, s))
+    assert len(seen) == len(set(seen))
+    assert set(seen) == {(b, s) for b in range(cfg.B) for s in range(ql[b])}
+
+
+def test_prefill_spreads_over_all_cores():
+    """8K SCFA prefill uses all 24 cores (test_sparse_attn_sharedkv.py:896-924);
+    a B=1 decode collapses onto one core."""
+    md, _ = _meta_for(C.REF_SCENARIOS["scfa_prefill"])
+    assert int(md[: AIC_CORE_NUM * FA_METADATA_SIZE].view(AIC_CORE_NUM, 8)[:, 0].sum()) == 24
+    md, _ = _meta_for(C.REF_SCENARIOS["scfa_decode"])
+    assert int(md[: AIC_CORE_NUM * FA_METADATA_SIZE].view(AIC_CORE_NUM, 8)[:, 0].sum()) == 1
+
+
+def test_scheduler_rejects_bad_heads():
+    with pytest.raises(ValueError):
+        sparse_attn_sharedkv_metadata(num_heads_q=64, num_heads_kv=0, head_dim=512,
+                                      seqused_kv=torch.tensor([10], dtype=torch.int32),
+                                      batch_size=1, max_seqlen_q=1, max_seqlen_kv=10)
+
+
+def test_scheduler_device_argument():
+    md = sparse_attn_sharedkv_metadata(num_heads_q=64, num_heads_kv=1, head_dim=512,
+                                       seqused_kv=torch.tensor([300], dtype=torch.int32),
+                                       batch_size=1, max_seqlen_q=1, max_seqlen_kv=300,
+                                       device="cpu")
+    assert md.device.type == "cpu" and md[0] == 1

@@ -1,0 +1,238 @@
+"""Pins of the attention oracle (CPU). Each check uses a formulation other
+than the oracle's chunked loop, chosen so a dropped term, wrong sign, wrong
+window bound or transposed operand fails one of them."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dsv4_amd import paged
+from oracle import golden_ref as O
+
+
+def test_online_softmax_worked_example():
+    """OnlineSoftmax 原理详解.md:332-378, 462-486: scores [1,3,2,5,4,0],
+    V [10..60]: 40.038 without a sink, 38.813 with sink 2 (d = 1.6278)."""
+    scores = torch.tensor([1.0, 3, 2, 5, 4, 0])
+    vals = torch.tensor([10.0, 20, 30, 40, 50, 60])
+    # one head, D = 2: k_j = [score_j, v_j] with q = [1, 0] and scale 1, so
+    # q.k = score; V is column 1 (dv slicing is exercised separately).
+    k = torch.stack([scores, vals], dim=1)
+    q = torch.tensor([[1.0, 0.0]])
+    for sink, want in ((-1e30, 40.038), (2.0, 38.813)):
+        # two tiles of 3 keys, like the worked example
+        num = torch.zeros(1)
+        out, lse = O._attend(q, [k[:3], k[3:]], torch.tensor([sink]), 1.0, torch.float32, 2)
+        assert abs(out[0, 1].item() - want) < 5e-3
+        if sink > -1e29:
+            assert abs(lse.item() - (5 + math.log(1.6278))) < 1e-3
+        del num
+
+
+def _rand_case(g, S=5, S2=300, D=64, K=12, ratio=4, G=4, win=31):
+    q = torch.randn(S, G, D, generator=g)
+    ori = torch.randn(S2, D, generator=g)
+    cmp_ = torch.randn(S2 // ratio, D, generator=g)
+    sinks = torch.randn(G, generator=g)
+    idx = torch.full((S, K), -1, dtype=torch.int32)
+    for s in range(S):
+        thr = (S2 - S + s + 1) // ratio
+        take = min(thr, K)
+        idx[s, :take] = torch.randperm(thr, generator=g)[:take].to(torch.int32)
+    return q, ori, cmp_, sinks, idx
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_closed_form_matches_brute_force_fp64(seed):
+    """softmax-with-sink closed form on the gathered keys == fp64 masked
+    formulation over ALL positions with the rule-derived 0/1 mask."""
+    g = torch.Generator().manual_seed(seed)
+    S, S2, D, ratio, win = 5, 300, 64, 4, 31
+    q, ori, cmp_, sinks, idx = _rand_case(g, S=S, S2=S2, D=D, ratio=ratio, win=win)
+    scale = 0.1
+    bf, bl = O.brute_force_fp64(q, ori, cmp_, idx, sinks, act_q=S, act_kv=S2, scale=scale,
+                                cmp_ratio=ratio, win_left=win, dv=48)
+    for s in range(S):
+        sg = S2 - S + s
+        thr = (sg + 1) // ratio
+        sel = [int(j) for j in idx[s] if 0 <= j < thr]
+        keys = torch.cat([ori[max(sg - win, 0):sg + 1], cmp_[sel]])
+        out, lse = O.sinks_softmax_closed_form(q[s].double(), keys.double(), sinks=sinks,
+                                               softmax_scale=scale, dv=48)
+        # the closed form computes in fp32 (golden.py:228-229)
+        torch.testing.assert_close(out.double(), bf[s], atol=1e-5, rtol=1e-5)
+        torch.testing.assert_close(lse.double(), bl[s], atol=1e-5, rtol=1e-5)
+
+
+def test_chunked_oracle_matches_closed_form():
+    """Chunked online softmax (tile 512 and tile 7) == one-shot softmax with the
+    sink, in fp32 (the reference's own check, test_sparse_attn_sharedkv.py:930-1002)."""
+    g = torch.Generator().manual_seed(7)
+    B, S, N1, D, ratio, K = 1, 6, 8, 96, 4, 40
+    S2 = 700
+    q = torch.randn(B, N1, S, D, generator=g)
+    ori = torch.randn(B, 1, S2, D, generator=g)
+    cmp_ = torch.randn(B, 1, S2 // ratio, D, generator=g)
+    sinks = torch.randn(N1, generator=g)
+    idx = torch.full((B, S, 1, K), -1, dtype=torch.int32)
+    for s in range(S):
+        thr = (S2 - S + s + 1) // ratio
+        idx[0, s, 0, :min(thr, K)] = torch.randperm(thr, generator=g)[:min(thr, K)].to(torch.int32)
+    for tile in (512, 7):
+        out, lse = O.golden_bnsd(q, ori, sinks, act_q_lens=[S], act_kv_lens=[S2],
+                                 softmax_scale=D ** -0.5, cmp_k_bnsd=cmp_,
+                                 cmp_sparse_indices=idx, cmp_ratio=ratio, dv=80, s2_tile=tile)
+        for s in range(S):
+            sg = S2 - S + s
+            thr = (sg + 1) // ratio
+            sel = [int(j) for j in idx[0, s, 0] if 0 <= j < thr]
+            keys = torch.cat([ori[0, 0, max(sg - 127, 0):sg + 1], cmp_[0, 0, sel]])
+            ref, ref_lse = O.sinks_softmax_closed_form(q[0, :, s], keys, sinks=sinks,
+                                                       softmax_scale=D ** -0.5, dv=80)
+            torch.testing.assert_close(out[0, :, s], ref, rtol=2e-4, atol=2e-4)
+            torch.testing.assert_close(lse[0, :, s], ref_lse, rtol=1e-4, atol=1e-4)
+
+
+def test_cfa_and_swa_modes_match_brute_force():
+    g = torch.Generator().manual_seed(3)
+    S, S2, D, ratio, win = 4, 200, 32, 8, 127
+    q, ori, cmp_, sinks, _ = _rand_case(g, S=S, S2=S2, D=D, ratio=ratio, win=win)
+    scale = 0.2
+    qb = q.permute(1, 0, 2).unsqueeze(0)
+    out, lse = O.golden_bnsd(qb, ori[None, None], sinks, act_q_lens=[S], act_kv_lens=[S2],
+                             softmax_scale=scale, cmp_k_bnsd=cmp_[None, None], cmp_ratio=ratio,
+                             dv=D)
+    bf, bl = O.brute_force_fp64(q, ori, cmp_, None, sinks, act_q=S, act_kv=S2, scale=scale,
+                                cmp_ratio=ratio, win_left=win, dv=D)
+    torch.testing.assert_close(out[0].permute(1, 0, 2).double(), bf, atol=2e-4, rtol=2e-4)
+    torch.testing.assert_close(lse[0].T.double(), bl, atol=2e-4, rtol=2e-4)
+    # SWA: no compressed rows at all
+    out, lse = O.golden_bnsd(qb, ori[None, None], sinks, act_q_lens=[S], act_kv_lens=[S2],
+                             softmax_scale=scale, dv=D)
+    bf, bl = O.brute_force_fp64(q, ori, cmp_[:0], None, sinks, act_q=S, act_kv=S2, scale=scale,
+                                cmp_ratio=ratio, win_left=win, dv=D)
+    torch.testing.assert_close(lse[0].T.double(), bl, atol=2e-4, rtol=2e-4)
+
+
+def test_paged_gather_equals_dense():
+    """Reading rows through shuffled block tables == reading the dense tensor
+    (golden.py:247-268 unpack invariant)."""
+    torch.manual_seed(0)
+    B, N1, D, ratio, K, bs = 2, 16, 64, 4, 16, 16
+    kv_lens = [300, 170]
+    q_lens = [3, 1]
+    ori_pa, ori_bt, ori_dense = paged.gen_ori_kv_paged(
+        B=B, N2=1, D=D, block_num=40, block_size=bs, seqused_kv=kv_lens, dtype=torch.float32,
+        rng=np.random.default_rng(1))
+    cmp_pa, cmp_bt, cmp_dense, _ = paged.gen_cmp_kv_paged(
+        B=B, N2=1, D=D, block_num=12, block_size=bs, seqused_kv=kv_lens, cmp_ratio=ratio,
+        dtype=torch.float32, rng=np.random.default_rng(2))
+    cu = torch.tensor([0, 3, 4], dtype=torch.int32)
+    idx = paged.gen_cmp_sparse_indices_tnd(B=B, T1=4, N2=1, K=K, cu_seqlens_q=cu,
+                                           seqused_kv=kv_lens, cmp_ratio=ratio,
+                                           rng=torch.Generator().manual_seed(5))
+    q = torch.randn(4, N1, D)
+    sinks = torch.randn(N1)
+    out, lse = O.golden_paged(q, ori_kv=ori_pa, ori_block_table=ori_bt, cu_seqlens_q=cu,
+                              seqused_kv=torch.tensor(kv_lens), sinks=sinks, softmax_scale=0.125,
+                              cmp_kv=cmp_pa, cmp_block_table=cmp_bt, cmp_sparse_indices=idx,
+                              cmp_ratio=ratio, dv=D)
+    qb = paged.tnd_to_bnsd_q(q, cu)
+    idx_b = torch.full((B, 3, 1, K), -1, dtype=torch.int32)
+    idx_b[0, :3] = idx[0:3]
+    idx_b[1, :1] = idx[3:4]
+    ob, lb = O.golden_bnsd(qb, ori_dense, sinks, act_q_lens=q_lens, act_kv_lens=kv_lens,
+                           softmax_scale=0.125, cmp_k_bnsd=cmp_dense, cmp_sparse_indices=idx_b,
+                           cmp_ratio=ratio, dv=D)
+    torch.testing.assert_close(out, paged.bnsd_to_tnd_out(ob, cu))
+    torch.testing.assert_close(lse, paged.bnsd_to_tnd_lse(lb, cu))
+    # and the dense copy really is what the pages hold
+    unpacked = paged.unpack_paged_kv(ori_pa, ori_bt, 300)
+    for b, n in enumerate(kv_lens):
+        torch.testing.assert_close(unpacked[b, :, :n], ori_dense[b, :, :n])
+
+
+def test_dv_slice_is_column_separable():
+    """Oracle at D_qk=576 with dv=512 equals golden at 576 sliced to 512."""
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(1, 4, 2, 576, generator=g).to(torch.bfloat16)
+    ori = torch.randn(1, 1, 90, 576, generator=g).to(torch.bfloat16)
+    sinks = torch.randn(4, generator=g)
+    full, lf = O.golden_bnsd(q, ori, sinks, act_q_lens=[2], act_kv_lens=[90],
+                             softmax_scale=576 ** -0.5)
+    cut, lc = O.golden_bnsd(q, ori, sinks, act_q_lens=[2], act_kv_lens=[90],
+                            softmax_scale=576 ** -0.5, dv=512)
+    assert torch.equal(full[..., :512], cut)
+    assert torch.equal(lf, lc)
+
+
+def test_golden_list_walk_stops_at_first_unused_slot():
+    """golden.py:48-62 walks only the first min(K, threshold) entries and stops
+    at the first -1; entries past it are ignored even if valid."""
+    assert O._cmp_rows([3, 1, -1, 2], threshold=10, cmp_len=50) == [3, 1]
+    assert O._cmp_rows([3, 9, 1], threshold=2, cmp_len=50) == []
+    assert O._cmp_rows([0, 5, 1, 1], threshold=4, cmp_len=50) == [0, 1, 1]
+
+
+def test_planted_mistakes_are_caught():
+    """Mutated oracles (sink dropped, window one row short) fail the pins."""
+    g = torch.Generator().manual_seed(5)
+    S, S2, D, ratio, win = 3, 150, 16, 4, 31
+    q, ori, cmp_, sinks, idx = _rand_case(g, S=S, S2=S2, D=D, ratio=ratio, win=win)
+    bf, bl = O.brute_force_fp64(q, ori, cmp_, idx, sinks, act_q=S, act_kv=S2, scale=0.3,
+                                cmp_ratio=ratio, win_left=win, dv=D)
+    sg = S2 - S
+    thr = (sg + 1) // ratio
+    sel = [int(j) for j in idx[0] if 0 <= j < thr]
+    good = torch.cat([ori[sg - win:sg + 1], cmp_[sel]])
+    short = torch.cat([ori[sg - win + 1:sg + 1], cmp_[sel]])
+    o_ok, l_ok = O.sinks_softmax_closed_form(q[0].double(), good.double(), sinks=sinks,
+                                             softmax_scale=0.3)
+    o_short, _ = O.sinks_softmax_closed_form(q[0].double(), short.double(), sinks=sinks,
+                                             softmax_scale=0.3)
+    o_nosink, l_nosink = O.sinks_softmax_closed_form(q[0].double(), good.double(),
+                                                     sinks=torch.full_like(sinks, -1e30),
+                                                     softmax_scale=0.3)
+    torch.testing.assert_close(o_ok.double(), bf[0], atol=1e-5, rtol=1e-5)
+    assert not torch.allclose(o_short.double(), bf[0], atol=1e-4)
+    assert not torch.allclose(l_nosink.double(), bl[0], atol=1e-4)
+
+
+def test_fp8_row_codec_roundtrip():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(7, 3, 576, generator=g) * 3
+    rows = paged.quantize_kv_fp8(x)
+    assert rows.shape == (7, 3, 656) and rows.dtype == torch.uint8
+    y = paged.dequantize_kv_fp8(rows)
+    # rope channels: bf16 rounding only
+    torch.testing.assert_close(y[..., 512:], x[..., 512:].to(torch.bfloat16).float())
+    # latent: e4m3 has 3 mantissa bits -> relative step 2^-3 at worst
+    lat, ref = y[..., :512], x[..., :512]
+    amax = ref.reshape(7, 3, 4, 128).abs().amax(-1, keepdim=True)
+    err = (lat - ref).reshape(7, 3, 4, 128).abs()
+    assert bool((err <= amax / 448 * 2 ** -4 * 448 / 8 + 1e-6).all()) or bool((err <= 0.0625 * ref.reshape(7, 3, 4, 128).abs() + amax / 448 * 2 ** -9 + 1e-6).all())
+    # exact re-encoding: decode(encode(decode(r))) == decode(r)
+    y2 = paged.dequantize_kv_fp8(paged.quantize_kv_fp8(y))
+    torch.testing.assert_close(y2, y, atol=0, rtol=1e-6)
+    # scale bytes decode to amax / 448
+    sc = rows[..., 512:528].contiguous().view(torch.float32)
+    torch.testing.assert_close(sc, amax.squeeze(-1) / 448)
+
+
+def test_index_generators_are_prefix_valid():
+    cu = torch.tensor([0, 1, 3, 7], dtype=torch.int32)
+    kv = [40, 9, 300]
+    idx = paged.gen_cmp_sparse_indices_tnd(B=3, T1=7, N2=1, K=16, cu_seqlens_q=cu, seqused_kv=kv,
+                                           cmp_ratio=4, rng=torch.Generator().manual_seed(0))
+    for b in range(3):
+        aq = int(cu[b + 1] - cu[b])
+        for s in range(aq):
+            row = idx[int(cu[b]) + s, 0].tolist()
+            thr = (kv[b] - aq + s + 1) // 4
+            n = min(thr, 16)
+            assert all(0 <= v < thr for v in row[:n]) and len(set(row[:n])) == n
+            assert all(v == -1 for v in row[n:])
