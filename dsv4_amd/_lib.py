@@ -57,6 +57,7 @@ class SasFwdArgs(C.Structure):
         ("cmp_ratio", C.c_int32), ("win_left", C.c_int32),
         ("softmax_scale", C.c_float),
         ("num_splits", C.c_int32),
+        ("head_waves", C.c_int32),
     ]
 
 

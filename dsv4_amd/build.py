@@ -23,7 +23,10 @@ HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # packed fp32 VALU forms are kept out of generated code on this pool
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wno-unused-result",
+    # keep MFMA accumulators in arch VGPRs: with AGPR accumulators the register
+    # allocator inserts AGPR<->VGPR copies on every loop back-edge
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
+    "-Wno-unused-result", "-Wno-inline-asm",
 ]
 
 

@@ -112,6 +112,9 @@ typedef struct SasFwdArgs {
   int32_t win_left;              /* ori_win_left (window = win_left + 1 rows) */
   float softmax_scale;
   int32_t num_splits;            /* KV splits per token; 0 = choose automatically */
+  int32_t head_waves;            /* waves sharing each KV tile (16 heads each): 1, 2, 4;
+                                    the other 4/head_waves groups stream disjoint rows;
+                                    0 = choose automatically */
 } SasFwdArgs;
 
 /*
