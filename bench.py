@@ -1,13 +1,20 @@
 """Benchmark of sparse_attn_sharedkv on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-traffic]
 
-Prints ONE JSON line. The headline workload is BASELINE config 2 (batched
-decode B=32, H=64, top-k 512 + window 128, ctx U[8K,32K], bf16, paged
-bs=64); `value` is its gathered-KV throughput in GB/s (valid window + top-k
-rows x 1152 B, counted once per token since all heads share the row).
-The 4K prefill (config 3) is reported beside it in TFLOP/s of useful work
-(valid (token, key) pairs x H x 2 x (576 + 512)).
+Prints ONE JSON line. The headline workload is config C2 (batched decode
+B=32, H=64, top-k 512 + window 128, ctx U[8K,32K], bf16, paged bs=64);
+`value` is its gathered-KV throughput in GB/s per whole call (split kernel +
+LSE combine): valid window + top-k rows x 1152 B, counted once per token
+since all heads share the row. The 4K prefill (C3) is reported beside it in
+TFLOP/s of useful work (valid (token, key) pairs x H x 2 x (576 + 512)).
+
+`roofline` prices the dominant kernel (the split-KV forward kernel of C2)
+alone: the same algorithmic bytes divided by its own event-timed average
+launch duration. `roofline.traffic` is the HBM bytes one launch of that
+kernel moves, from two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE)
+run as child processes of this script, each scaled by what the same counter
+reads for an elementwise kernel of known size (`--pmc-pass` is that child).
 
 Decode inputs rotate over copies whose touched rows together exceed the
 256 MB Infinity Cache, so each call reads HBM, not MALL. Inputs are resident
@@ -18,9 +25,15 @@ restatement of the reference's golden loop) on the host cores.
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
+import signal
+import subprocess
 import sys
+import tempfile
 import time
 
 import torch
@@ -28,6 +41,11 @@ import torch
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 METRIC = "decode µs/call + HBM GB/s (B32,H64,k512+w128); prefill TFLOP/s at 4K"
+SPLIT_KERNEL = "sas_fwd_kernel"
+COMBINE_KERNEL = "sas_combine_kernel"
+CAL_KERNEL = "neg_kernel"      # torch.neg on fp32: reads and writes numel*4 bytes
+CAL_NUMEL = 32 << 20           # 128 MiB each way
+PMC_ROTATIONS = 4              # 94 MB of gathered rows: beyond the 32 MB of L2
 
 
 def log(msg):
@@ -49,30 +67,34 @@ def _rotations(inp, n):
     return out
 
 
-def time_calls(calls, steps, warmup):
-    """Launch calls[i % n] `steps` times between two synchronisations; returns
-    (total ms from events on the launch stream, wall ms)."""
+def time_launches(launch, n_calls, steps, warmup):
+    """Run launch(i, stream) for i in [0, steps) between two synchronisations
+    (after `warmup` untimed calls); events are recorded on the launch stream.
+    Returns (total event ms, wall ms)."""
     st = torch.cuda.current_stream()
     for i in range(warmup):
-        calls[i % len(calls)].launch(st)
+        launch(i % n_calls, st)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(st)
     for i in range(steps):
-        calls[i % len(calls)].launch(st)
+        launch(i % n_calls, st)
     e1.record(st)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3
     return e0.elapsed_time(e1), wall
 
 
-def cpu_oracle_time(inp, tokens=None, reps=1):
+def cpu_oracle_time(inp, tokens=None, min_seconds=0.0, max_reps=1):
+    """Median seconds of one oracle pass; repeats until min_seconds of CPU
+    work (or max_reps passes) have run."""
     from oracle import golden_ref as O
     from dsv4_amd import paged
     c = inp.cfg
     ts = []
-    for _ in range(reps):
+    t_start = time.perf_counter()
+    while True:
         t0 = time.perf_counter()
         O.golden_paged(inp.q, ori_kv=inp.ori_kv, ori_block_table=inp.ori_bt,
                        cu_seqlens_q=inp.cu_seqlens_q, seqused_kv=inp.seqused_kv, sinks=inp.sinks,
@@ -80,8 +102,96 @@ def cpu_oracle_time(inp, tokens=None, reps=1):
                        cmp_sparse_indices=inp.cmp_idx, cmp_ratio=c.cmp_ratio, dv=512,
                        dequant=paged.dequantize_kv_fp8 if c.fp8 else None, tokens=tokens)
         ts.append(time.perf_counter() - t0)
+        if len(ts) >= max_reps or time.perf_counter() - t_start >= min_seconds:
+            break
     ts.sort()
-    return ts[len(ts) // 2]
+    return ts[len(ts) // 2], len(ts), time.perf_counter() - t_start
+
+
+# ---------------------------------------------------------------------------
+# HBM traffic from rocprofv3 --pmc (child processes)
+# ---------------------------------------------------------------------------
+
+def pmc_pass():
+    """Child of a `rocprofv3 --pmc` run: a calibration kernel of known size,
+    then PMC_ROTATIONS rounds of C2 decode (split kernel + combine) over
+    distinct input copies."""
+    from dsv4_amd import cases
+    torch.cuda.init()
+    src = torch.randn(CAL_NUMEL, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    inp = cases.make_inputs(cases.CONFIGS["C2"], device="cuda")
+    calls = [_prepare(r) for r in _rotations(inp, PMC_ROTATIONS)]
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for c in calls:
+            c.launch_split()
+            c.launch_combine()
+    torch.cuda.synchronize()
+    print("[pmc-pass] done", flush=True)
+
+
+def _read_counter(outdir, counter):
+    """{kernel substring: [per-dispatch values]} for the counter."""
+    vals = {SPLIT_KERNEL: [], COMBINE_KERNEL: [], CAL_KERNEL: []}
+    files = glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True)
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row.get("Kernel_Name", "")
+                for k in vals:
+                    if k in name:
+                        vals[k].append(float(row["Counter_Value"]))
+    return vals
+
+
+def measure_traffic(kv_bytes_hint=None):
+    """HBM bytes per launch of the split kernel (and the combine), each of the
+    two counters scaled by its reading for the calibration kernel."""
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None, "rocprofv3 not found"
+    res = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        outdir = tempfile.mkdtemp(prefix="sas_pmc_")
+        cmd = [prof, "--pmc", counter, "-d", outdir, "-o", "pmc", "--output-format", "csv",
+               "--", sys.executable, os.path.abspath(__file__), "--pmc-pass"]
+        log(f"pmc pass {counter}")
+        p = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                             start_new_session=True)
+        try:
+            text, _ = p.communicate(timeout=150)
+        except subprocess.TimeoutExpired:
+            os.killpg(p.pid, signal.SIGKILL)
+            p.communicate()
+            shutil.rmtree(outdir, ignore_errors=True)
+            return None, f"rocprofv3 --pmc {counter} timed out"
+        vals = _read_counter(outdir, counter)
+        shutil.rmtree(outdir, ignore_errors=True)
+        if "[pmc-pass] done" not in text or not vals[SPLIT_KERNEL] or not vals[CAL_KERNEL]:
+            tail = " | ".join(text.strip().splitlines()[-3:])
+            return None, f"rocprofv3 --pmc {counter} gave no usable rows (rc {p.returncode}): {tail}"
+        res[counter] = vals
+    out = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        v = res[counter]
+        cal = sorted(v[CAL_KERNEL])[len(v[CAL_KERNEL]) // 2] * 1024.0 / (CAL_NUMEL * 4)
+        # skip the first pass over the rotations (cold TLB / first touch)
+        split = v[SPLIT_KERNEL][PMC_ROTATIONS:] or v[SPLIT_KERNEL]
+        comb = v[COMBINE_KERNEL][PMC_ROTATIONS:] or v[COMBINE_KERNEL]
+        out[counter] = dict(
+            cal_factor=round(cal, 4),
+            split_bytes=sum(split) / len(split) * 1024.0 / cal,
+            combine_bytes=(sum(comb) / len(comb) * 1024.0 / cal) if comb else None)
+    return out, None
+
+
+# ---------------------------------------------------------------------------
 
 
 def main():
@@ -93,11 +203,23 @@ def main():
     ap.add_argument("--rotations", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this operator build runs on a single MI355X "
               "(multi-GPU sharding is a design note, not a measured path)", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_pass:
+        pmc_pass()
+        return
+
+    # counter passes run first, in child processes, before this process
+    # touches the GPU
+    traffic, traffic_note = (None, "skipped (--no-traffic)")
+    if not args.no_traffic:
+        traffic, traffic_note = measure_traffic()
+        log(f"traffic: {traffic if traffic else traffic_note}")
 
     from dsv4_amd import cases
     if not torch.cuda.is_available():
@@ -115,13 +237,25 @@ def main():
     rot = _rotations(inp, args.rotations)
     calls = [_prepare(r) for r in rot]
     torch.cuda.synchronize()
-    log(f"C2: T={inp.T} gathered rows={rows} bytes={kv_bytes} splits={calls[0].num_splits} "
+    ns = calls[0].num_splits
+    log(f"C2: T={inp.T} gathered rows={rows} bytes={kv_bytes} splits={ns} "
         f"rotations={len(calls)} (touched {len(calls) * kv_bytes / 1e6:.0f} MB)")
-    ev_ms, wall_ms = time_calls(calls, args.steps, args.warmup)
+    ev_ms, wall_ms = time_launches(lambda i, st: calls[i].launch(st), len(calls),
+                                   args.steps, args.warmup)
     us_call = ev_ms * 1e3 / args.steps
     gbs = kv_bytes / (us_call * 1e-6) / 1e9
     log(f"C2 decode: {us_call:.2f} us/call (events), {wall_ms * 1e3 / args.steps:.2f} us wall, "
         f"{gbs:.0f} GB/s")
+    # the dominant kernel alone (split kernel, partials left in the workspace)
+    sp_ms, sp_wall = time_launches(lambda i, st: calls[i].launch_split(st), len(calls),
+                                   args.steps, args.warmup)
+    us_split = sp_ms * 1e3 / args.steps
+    cb_ms, _ = time_launches(lambda i, st: calls[i].launch_combine(st), len(calls),
+                             args.steps, args.warmup)
+    us_comb = cb_ms * 1e3 / args.steps
+    split_gbs = kv_bytes / (us_split * 1e-6) / 1e9
+    log(f"C2 split kernel: {us_split:.2f} us/launch ({sp_wall * 1e3 / args.steps:.2f} us wall), "
+        f"{split_gbs:.0f} GB/s; combine {us_comb:.2f} us/launch")
     # API wall time (host resolution + launch), reported separately
     from dsv4_amd.api import sparse_attn_sharedkv
     kw = inp.api_kwargs()
@@ -143,7 +277,7 @@ def main():
         prows = cases.gathered_rows(pinp)
         flops = prows * pcfg.H * 2 * (pcfg.D + pcfg.DV)
         pcall = _prepare(pinp)
-        pev, _ = time_calls([pcall], args.prefill_steps, 3)
+        pev, _ = time_launches(lambda i, st: pcall.launch(st), 1, args.prefill_steps, 3)
         pus = pev * 1e3 / args.prefill_steps
         tfl = flops / (pus * 1e-6) / 1e12
         prefill = dict(workload="C3 prefill S4096 H64 k512+w128 contiguous", us_per_call=round(pus, 2),
@@ -158,17 +292,22 @@ def main():
         torch.set_num_threads(n)
         log(f"CPU baseline on {n} threads")
         host = inp.to("cpu")
-        cpu_s = cpu_oracle_time(host, reps=3)
+        cpu_s, reps, spent = cpu_oracle_time(host, min_seconds=10.0, max_reps=1000)
         cpu = dict(value=round(kv_bytes / cpu_s / 1e9, 3), unit="GB/s", cores=n, kind="port",
                    us_per_call=round(cpu_s * 1e6, 1),
-                   sample="full C2 decode call (32 tokens), median of 3, torch fp32 oracle")
+                   sample=f"full C2 decode call (32 tokens x 64 heads), median of {reps} calls "
+                          f"({spent:.1f} s), torch fp32 oracle")
         if prefill is not None:
             ph = pinp.to("cpu")
-            toks = list(range(0, pinp.T, 16))
-            ps = cpu_oracle_time(ph, tokens=toks) * pinp.T / len(toks)
+            toks = list(range(0, pinp.T, 8))
+            ps1, _, _ = cpu_oracle_time(ph, tokens=toks)
+            ps = ps1 * pinp.T / len(toks)
             cpu["prefill_tflops"] = round(prefill["useful_flop"] / ps / 1e12, 4)
-            cpu["prefill_sample"] = f"{len(toks)} of {pinp.T} C3 tokens (every 16th), scaled"
+            cpu["prefill_sample"] = f"{len(toks)} of {pinp.T} C3 tokens (every 8th), scaled"
 
+    tr = None
+    if traffic:
+        tr = round(traffic["FETCH_SIZE"]["split_bytes"] + traffic["WRITE_SIZE"]["split_bytes"])
     line = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -186,11 +325,15 @@ def main():
                                "ctx U[8K,32K], paged bs64", "B": 32, "H": 64, "topk": 512,
                    "window": 128, "parallelism": "single GPU"},
         "decode_us_per_call": round(us_call, 3),
+        "split_kernel_us": round(us_split, 3),
+        "combine_kernel_us": round(us_comb, 3),
+        "num_splits": ns,
         "api_us_per_call": round(api_us, 1),
         "gathered_kv_bytes": kv_bytes,
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel_time": "event-timed op (fwd + split combine) per call"},
+        "roofline": {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": tr,
+                     "kernel": f"{SPLIT_KERNEL} (C2 split-KV forward, {ns} splits)",
+                     "traffic_detail": traffic if traffic else traffic_note},
         "prefill": prefill,
         "cpu_baseline": cpu,
     }

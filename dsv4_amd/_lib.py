@@ -17,6 +17,7 @@ SAS_OK, SAS_EINVAL, SAS_ELAUNCH, SAS_ENOWS = 0, 1, 2, 3
 SAS_DT_BF16, SAS_DT_FP16, SAS_DT_FP8_E4M3_ROW656 = 0, 1, 2
 SAS_SWA, SAS_CFA, SAS_SCFA = 1, 2, 3
 SAS_META_SIZE = 1024
+SAS_FWD_NO_COMBINE = 1
 
 EXPORTED = ("sas_metadata_v1", "sas_fwd_plan", "sas_fwd_v1", "sas_combine_v1",
             "sas_last_error", "sas_version")
@@ -58,6 +59,7 @@ class SasFwdArgs(C.Structure):
         ("softmax_scale", C.c_float),
         ("num_splits", C.c_int32),
         ("head_waves", C.c_int32),
+        ("flags", C.c_int32),
     ]
 
 

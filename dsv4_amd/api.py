@@ -63,10 +63,43 @@ class PreparedCall:
             args.workspace_bytes = ws.value
         args.num_splits = self.num_splits
 
-    def launch(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+    def _stream(self, stream):
         st = stream if stream is not None else torch.cuda.current_stream(self.out.device)
-        _lib.check(_lib.lib().sas_fwd_v1(C.byref(self.args), C.c_void_p(st.cuda_stream)),
+        return C.c_void_p(st.cuda_stream)
+
+    def launch(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Split kernel, then (with more than one split) the LSE combine."""
+        self.args.flags = 0
+        _lib.check(_lib.lib().sas_fwd_v1(C.byref(self.args), self._stream(stream)),
                    "sparse_attn_sharedkv")
+
+    def launch_split(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Split kernel only; with more than one split the result is the fp32
+        partials in :attr:`workspace` until :meth:`launch_combine` runs."""
+        self.args.flags = _lib.SAS_FWD_NO_COMBINE
+        try:
+            _lib.check(_lib.lib().sas_fwd_v1(C.byref(self.args), self._stream(stream)),
+                       "sparse_attn_sharedkv")
+        finally:
+            self.args.flags = 0
+
+    def combine_args(self) -> _lib.SasCombineArgs:
+        a = self.args
+        ca = _lib.SasCombineArgs()
+        ca.part_o = a.workspace
+        ca.part_ml = a.workspace + a.T * self.num_splits * a.H * a.DV * 4
+        ca.sinks, ca.out, ca.lse = a.sinks, a.out, a.lse
+        ca.T, ca.S, ca.H, ca.DV = a.T, self.num_splits, a.H, a.DV
+        ca.out_dtype = a.q_dtype
+        return ca
+
+    def launch_combine(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+        """LSE combine of the partials left by :meth:`launch_split`."""
+        if self.num_splits <= 1:
+            return
+        ca = self.combine_args()
+        _lib.check(_lib.lib().sas_combine_v1(C.byref(ca), self._stream(stream)),
+                   "sparse_attn_sharedkv combine")
 
     def result(self, return_softmax_lse: bool):
         out, lse = self.out, self.lse
@@ -100,6 +133,7 @@ def prepare_sparse_attn_sharedkv(
     core_num: int = DEFAULT_CORE_NUM,
     topk_cmp: Optional[int] = None,
     num_splits: int = 0,
+    head_waves: int = 0,
 ) -> PreparedCall:
     """Validate and resolve the arguments of :func:`sparse_attn_sharedkv`
     (api.py:186-366) and allocate outputs; see that function."""
@@ -246,6 +280,7 @@ def prepare_sparse_attn_sharedkv(
     a.win_left = int(ori_win_left)
     a.softmax_scale = float(softmax_scale)
     a.num_splits = int(num_splits)
+    a.head_waves = int(head_waves)
     return PreparedCall(a, keep, out, lse, layout_q, B, S_max)
 
 

@@ -45,6 +45,7 @@ constexpr int kTR = 32;           // rows per pipeline step
 constexpr int kDV = 512;          // output / V channels
 constexpr int kMaxSlots = 1280;   // slot range one workgroup may own
 constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dealt round-robin
+constexpr int kSplitTarget = 128; // workgroups the automatic split count aims for
 constexpr int kRow656 = 656;      // fp8 cache row bytes
 constexpr int kChunksMax = 72;    // 16-byte chunks of a 576-channel bf16 row
 constexpr int kSlotChunks = kTR * kChunksMax;
@@ -759,14 +760,15 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   if (a->DV != kDV) return sas::set_error(SAS_EINVAL, "DV must be 512 (got %lld)", (long long)a->DV);
   if (a->H % 16) return sas::set_error(SAS_EINVAL, "H must be a multiple of 16 (got %lld)", (long long)a->H);
   if (a->scenario < SAS_SWA || a->scenario > SAS_SCFA) return sas::set_error(SAS_EINVAL, "bad scenario");
+  if (a->flags & ~SAS_FWD_NO_COMBINE) return sas::set_error(SAS_EINVAL, "unknown flags 0x%x", a->flags);
   if (a->win_left < 0 || a->win_left > 8191) return sas::set_error(SAS_EINVAL, "win_left out of range");
   if (a->scenario >= SAS_CFA && (a->cmp_ratio < 1 || a->K < 0)) return sas::set_error(SAS_EINVAL, "bad cmp_ratio/K");
   const bool fp8 = a->kv_dtype == SAS_DT_FP8_E4M3_ROW656;
-  // head-waves per workgroup: 4 (64 heads share every tile) when there are
-  // enough (token, head-group) items to fill the chip, else 2 (two key-groups
-  // stream disjoint rows; fewer heads per workgroup, more workgroups).
+  // head-waves per workgroup: 4 whenever H allows it (64 heads share every
+  // gathered tile, so each KV row crosses HBM->LDS once per token); 2 or 1
+  // only for head counts that are not a multiple of 64.
   int hw = a->head_waves;
-  if (hw <= 0) hw = ((long long)a->T * (a->H / 64) >= 512) ? 4 : 2;
+  if (hw <= 0) hw = 4;
   if (hw != 1 && hw != 2 && hw != 4) return sas::set_error(SAS_EINVAL, "head_waves must be 1, 2 or 4");
   while (hw > 1 && a->H % (16 * hw)) hw >>= 1;
   if (fp8) {  // fp8 staging registers only fit with 4 head-waves (or 2 when H = 32k)
@@ -778,9 +780,12 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   pl->nslots = a->win_left + 1 + (a->scenario >= SAS_CFA ? (int)a->K : 0);
   int ns = a->num_splits;
   if (ns <= 0) {
-    // fill ~256 CUs with one workgroup each; splits no smaller than one step
+    // about half a workgroup per CU: every extra split adds a partial
+    // write + combine read of 2 KB per head, which past ~128 workgroups
+    // costs more than the extra streaming parallelism gains; splits no
+    // smaller than one 32-row step
     const long long items = std::max<long long>(1, (long long)a->T * pl->nhg);
-    const long long want = (256 + items - 1) / items;
+    const long long want = (kSplitTarget + items - 1) / items;
     const int max_by_step = std::max(1, (pl->nslots + kTR - 1) / kTR);
     ns = (int)std::min<long long>(std::max<long long>(want, 1), max_by_step);
   }
@@ -914,7 +919,7 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
     rc = a->D == 576 ? dispatch_hw<576, _Float16, 0>(pl.hw, fp, nblocks, st)
                      : dispatch_hw<512, _Float16, 0>(pl.hw, fp, nblocks, st);
   if (rc) return rc;
-  if (pl.nsplit > 1) {
+  if (pl.nsplit > 1 && !(a->flags & SAS_FWD_NO_COMBINE)) {
     SasCombineArgs ca;
     ca.part_o = fp.part_o; ca.part_ml = fp.part_ml; ca.sinks = a->sinks;
     ca.out = a->out; ca.lse = a->lse;

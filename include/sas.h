@@ -115,7 +115,14 @@ typedef struct SasFwdArgs {
   int32_t head_waves;            /* waves sharing each KV tile (16 heads each): 1, 2, 4;
                                     the other 4/head_waves groups stream disjoint rows;
                                     0 = choose automatically */
+  int32_t flags;                 /* SAS_FWD_* bits, 0 by default */
 } SasFwdArgs;
+
+/* SasFwdArgs.flags: with more than one split, stop after the split kernel and
+   leave the fp32 partials in the workspace (part_o at offset 0, part_ml after
+   T*S*H*DV floats, S = the planned split count); the caller then runs
+   sas_combine_v1 itself, e.g. to time or overlap the two kernels apart. */
+#define SAS_FWD_NO_COMBINE 1
 
 /*
  * Split count the library would use (after auto-selection) and the

@@ -52,27 +52,35 @@ def _cmp_rows(idx_row: Sequence[int], threshold: int, cmp_len: int) -> list:
     return rows
 
 
-def _attend(q: torch.Tensor, tiles, sinks: torch.Tensor, scale: float, dtype, dv: int):
+def _attend(q: torch.Tensor, tiles, sinks: torch.Tensor, scale: float, dtype, dv: int,
+            exact: bool = False):
     """Chunked sink-seeded online softmax for one token (golden.py:156-200).
 
     ``q`` [G, D] fp32, ``tiles`` list of fp32 [n, D] (already in walk order).
-    Returns (out [G, dv] in ``dtype``, lse [G] fp32).
+    Returns (out [G, dv] in ``dtype``, lse [G] fp32). With ``exact`` the same
+    walk runs in fp64 with no rounding of ``p`` or of the output (a reference
+    point for how far golden's own bf16/fp16 roundings move it).
     """
     G = q.shape[0]
-    m = sinks.clone()
-    l = torch.ones(G, dtype=torch.float32)
-    acc = torch.zeros((G, dv), dtype=torch.float32)
+    wt = torch.float64 if exact else torch.float32
+    q = q.to(wt)
+    m = sinks.to(wt).clone()
+    l = torch.ones(G, dtype=wt)
+    acc = torch.zeros((G, dv), dtype=wt)
     for k in tiles:
         if k.shape[0] == 0:
             continue
+        k = k.to(wt)
         sc = (q @ k.T) * scale
         m_new = torch.maximum(m, sc.amax(dim=1))
         alpha = torch.exp(m - m_new)
         p = torch.exp(sc - m_new.unsqueeze(1))
         l = alpha * l + p.sum(dim=1)
-        acc = acc * alpha.unsqueeze(1) + p.to(dtype).to(torch.float32) @ k[:, :dv]
+        pr = p if exact else p.to(dtype).to(torch.float32)
+        acc = acc * alpha.unsqueeze(1) + pr @ k[:, :dv]
         m = m_new
-    return (acc / l.unsqueeze(1)).to(dtype), m + torch.log(l)
+    o = acc / l.unsqueeze(1)
+    return (o if exact else o.to(dtype)), m + torch.log(l)
 
 
 def _tiles(rows: torch.Tensor, tile: int):
@@ -128,14 +136,15 @@ def _paged_rows(kv, bt_row, positions, dequant):
 def golden_paged(q, *, ori_kv, ori_block_table, cu_seqlens_q, seqused_kv, sinks,
                  softmax_scale, cmp_kv=None, cmp_block_table=None, cmp_sparse_indices=None,
                  cmp_ratio=None, ori_win_left=127, dv=512, dequant=None, tokens=None,
-                 s2_tile: int = GOLDEN_S2_TILE):
+                 s2_tile: int = GOLDEN_S2_TILE, exact: bool = False):
     """TND / paged-cache oracle: same math as :func:`golden_bnsd`, rows read
     through block tables (only the rows a token touches are materialised).
 
     ``q`` [T, H, D]; caches ``[nb, bs, 1, D]`` (or uint8 fp8 rows with
     ``dequant``); ``cmp_sparse_indices`` [T, 1, K] (SCFA) or None with
     ``cmp_kv`` given (CFA). ``tokens`` restricts the computation to a subset
-    of packed token ids (others stay zero). Returns (out [T, H, dv], lse [T, H]).
+    of packed token ids (others stay zero). Returns (out [T, H, dv], lse [T, H]);
+    with ``exact`` both are fp64 and unrounded (see :func:`_attend`).
     """
     q = q.cpu()
     T, H, D = q.shape
@@ -145,8 +154,8 @@ def golden_paged(q, *, ori_kv, ori_block_table, cu_seqlens_q, seqused_kv, sinks,
     ori_bt = ori_block_table.cpu()
     cmp_bt = cmp_block_table.cpu() if cmp_block_table is not None else None
     idx = cmp_sparse_indices.cpu() if cmp_sparse_indices is not None else None
-    out = torch.zeros((T, H, dv), dtype=dtype)
-    lse = torch.zeros((T, H), dtype=torch.float32)
+    out = torch.zeros((T, H, dv), dtype=torch.float64 if exact else dtype)
+    lse = torch.zeros((T, H), dtype=torch.float64 if exact else torch.float32)
     sinks = sinks.float().cpu()
     want = None if tokens is None else set(int(t) for t in tokens)
     for b in range(len(cu) - 1):
@@ -166,7 +175,7 @@ def golden_paged(q, *, ori_kv, ori_block_table, cu_seqlens_q, seqused_kv, sinks,
                 else:
                     sel = list(range(max(thr, 0)))
                 parts += _tiles(_paged_rows(cmp_kv, cmp_bt[b], sel, dequant), s2_tile)
-            o, l_ = _attend(q[t].float(), parts, sinks, softmax_scale, dtype, dv)
+            o, l_ = _attend(q[t].float(), parts, sinks, softmax_scale, dtype, dv, exact)
             out[t] = o
             lse[t] = l_
     return out, lse

@@ -1,0 +1,119 @@
+"""C ABI of libsas.so: every function include/sas.h declares is exported, and
+argument validation fails with the documented status codes before any
+device work (no GPU needed)."""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from dsv4_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(__file__), "..", "include", "sas.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(sas_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_exported_set():
+    assert _declared() == sorted(_lib.EXPORTED)
+
+
+@pytest.mark.parametrize("sym", _declared())
+def test_symbol_exported(sym):
+    assert hasattr(_lib.lib(), sym), f"libsas.so does not export {sym}"
+
+
+def test_version():
+    assert _lib.lib().sas_version().decode().startswith("libsas")
+
+
+def _valid_args(**over):
+    a = _lib.SasFwdArgs()
+    a.T, a.B, a.H, a.D, a.DV = 4, 1, 64, 576, 512
+    a.ori_block_size, a.ori_bt_stride, a.ori_num_blocks = 64, 8, 8
+    a.cmp_block_size, a.cmp_bt_stride, a.cmp_num_blocks = 64, 2, 2
+    a.K, a.scenario, a.q_dtype, a.kv_dtype = 64, _lib.SAS_SCFA, _lib.SAS_DT_BF16, _lib.SAS_DT_BF16
+    a.cmp_ratio, a.win_left, a.softmax_scale = 4, 127, 0.0417
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+def _plan(a):
+    ns, ws = C.c_int32(-1), C.c_size_t(0)
+    rc = _lib.lib().sas_fwd_plan(C.byref(a), C.byref(ns), C.byref(ws))
+    return rc, ns.value, ws.value
+
+
+def test_plan_valid():
+    rc, ns, ws = _plan(_valid_args())
+    assert rc == _lib.SAS_OK
+    assert ns >= 1
+    assert ws == (0 if ns == 1 else 4 * ns * 64 * (512 + 2) * 4)
+
+
+def test_plan_explicit_splits_and_workspace():
+    rc, ns, ws = _plan(_valid_args(num_splits=3))
+    assert rc == _lib.SAS_OK and ns == 3
+    assert ws == 4 * 3 * 64 * 514 * 4
+
+
+@pytest.mark.parametrize("field,value,needle", [
+    ("D", 128, "D must be 512 or 576"),
+    ("DV", 256, "DV must be 512"),
+    ("H", 40, "multiple of 16"),
+    ("scenario", 7, "scenario"),
+    ("win_left", -1, "win_left"),
+    ("head_waves", 3, "head_waves"),
+    ("flags", 0x10, "flags"),
+])
+def test_plan_rejects(field, value, needle):
+    rc, _, _ = _plan(_valid_args(**{field: value}))
+    assert rc == _lib.SAS_EINVAL
+    assert needle in _lib.lib().sas_last_error().decode()
+
+
+def test_fwd_rejects_null_pointers_without_device_work():
+    rc = _lib.lib().sas_fwd_v1(C.byref(_valid_args()), None)
+    assert rc == _lib.SAS_EINVAL
+    assert "null device pointer" in _lib.lib().sas_last_error().decode()
+
+
+def test_fwd_empty_batch_is_a_no_op():
+    assert _lib.lib().sas_fwd_v1(C.byref(_valid_args(T=0)), None) == _lib.SAS_OK
+    assert _lib.lib().sas_last_error().decode() == ""
+
+
+def test_fwd_missing_workspace():
+    a = _valid_args(num_splits=2)
+    fake = 1 << 40  # never dereferenced: validation fails first
+    for f in ("q", "ori_kv", "ori_block_table", "cmp_kv", "cmp_block_table", "cmp_indices",
+              "q_prefix", "act_q", "act_kv", "sinks", "out", "lse"):
+        setattr(a, f, fake)
+    assert _lib.lib().sas_fwd_v1(C.byref(a), None) == _lib.SAS_ENOWS
+    assert "workspace" in _lib.lib().sas_last_error().decode()
+
+
+def test_combine_rejects():
+    ca = _lib.SasCombineArgs()
+    assert _lib.lib().sas_combine_v1(C.byref(ca), None) == _lib.SAS_EINVAL
+    fake = 1 << 40
+    ca.part_o = ca.part_ml = ca.sinks = ca.out = ca.lse = fake
+    ca.T, ca.S, ca.H, ca.DV, ca.out_dtype = 1, 65, 64, 512, _lib.SAS_DT_BF16
+    assert _lib.lib().sas_combine_v1(C.byref(ca), None) == _lib.SAS_EINVAL
+    assert "S must be" in _lib.lib().sas_last_error().decode()
+
+
+def test_check_maps_status_to_exceptions():
+    _lib.lib().sas_fwd_plan(C.byref(_valid_args(D=1)), None, None)
+    with pytest.raises(ValueError, match="D must be"):
+        _lib.check(_lib.SAS_EINVAL, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.SAS_ELAUNCH, "x")

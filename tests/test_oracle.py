@@ -156,6 +156,39 @@ def test_paged_gather_equals_dense():
         torch.testing.assert_close(unpacked[b, :, :n], ori_dense[b, :, :n])
 
 
+def test_exact_mode_matches_brute_force_fp64():
+    """golden_paged(exact=True) (fp64, no rounding of p) == the independent fp64
+    masked formulation, to fp64 round-off; the default mode (p rounded to
+    bf16, as golden.py:189) is measurably further away."""
+    S2, D, ratio, K, bs, N1, S = 260, 64, 4, 24, 16, 8, 3
+    ori_pa, ori_bt, ori_dense = paged.gen_ori_kv_paged(
+        B=1, N2=1, D=D, block_num=20, block_size=bs, seqused_kv=[S2], dtype=torch.bfloat16,
+        rng=np.random.default_rng(3))
+    cmp_pa, cmp_bt, cmp_dense, _ = paged.gen_cmp_kv_paged(
+        B=1, N2=1, D=D, block_num=6, block_size=bs, seqused_kv=[S2], cmp_ratio=ratio,
+        dtype=torch.bfloat16, rng=np.random.default_rng(4))
+    cu = torch.tensor([0, S], dtype=torch.int32)
+    idx = paged.gen_cmp_sparse_indices_tnd(B=1, T1=S, N2=1, K=K, cu_seqlens_q=cu,
+                                           seqused_kv=[S2], cmp_ratio=ratio,
+                                           rng=torch.Generator().manual_seed(6))
+    g = torch.Generator().manual_seed(8)
+    q = torch.randn(S, N1, D, generator=g).to(torch.bfloat16)
+    sinks = torch.randn(N1, generator=g)
+    kw = dict(ori_kv=ori_pa, ori_block_table=ori_bt, cu_seqlens_q=cu,
+              seqused_kv=torch.tensor([S2]), sinks=sinks, softmax_scale=0.3, cmp_kv=cmp_pa,
+              cmp_block_table=cmp_bt, cmp_sparse_indices=idx, cmp_ratio=ratio, dv=D,
+              ori_win_left=31)
+    ex, exl = O.golden_paged(q, exact=True, **kw)
+    rd, _ = O.golden_paged(q, **kw)
+    bf, bl = O.brute_force_fp64(q.double(), ori_dense[0, 0].double(), cmp_dense[0, 0].double(),
+                                idx[:, 0], sinks, act_q=S, act_kv=S2, scale=0.3,
+                                cmp_ratio=ratio, win_left=31, dv=D)
+    assert ex.dtype == torch.float64
+    torch.testing.assert_close(ex, bf, atol=1e-10, rtol=1e-10)
+    torch.testing.assert_close(exl, bl, atol=1e-10, rtol=1e-10)
+    assert (rd.double() - bf).abs().max() > 1e-4
+
+
 def test_dv_slice_is_column_separable():
     """Oracle at D_qk=576 with dv=512 equals golden at 576 sliced to 512."""
     g = torch.Generator().manual_seed(11)
