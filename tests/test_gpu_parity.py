@@ -184,7 +184,7 @@ def test_reference_scenarios(name, s1, dtype):
     print(f"[parity] {name} {dtype}: splits={ns} mean|err| vs fp64: ours {e_ours:.4g} "
           f"golden {e_gold:.4g}", flush=True)
     assert e_ours <= 1.10 * e_gold + 1e-6, f"{name}: less accurate than golden"
-    torch.testing.assert_close(lse.double(), ex_lse, atol=0.0, rtol=2e-6)
+    torch.testing.assert_close(lse.double(), ex_lse, atol=1e-5, rtol=2e-6)
     if dtype == torch.bfloat16:
         rules = [(out, ref_out, 0.0078125, 1e-4, "out"), (lse, ref_lse, 0.015, 0.005, "lse")]
     else:
