@@ -60,6 +60,7 @@ class SasFwdArgs(C.Structure):
         ("num_splits", C.c_int32),
         ("head_waves", C.c_int32),
         ("flags", C.c_int32),
+        ("waves", C.c_int32),
     ]
 
 

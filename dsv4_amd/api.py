@@ -134,6 +134,7 @@ def prepare_sparse_attn_sharedkv(
     topk_cmp: Optional[int] = None,
     num_splits: int = 0,
     head_waves: int = 0,
+    waves: int = 0,
 ) -> PreparedCall:
     """Validate and resolve the arguments of :func:`sparse_attn_sharedkv`
     (api.py:186-366) and allocate outputs; see that function."""
@@ -281,6 +282,7 @@ def prepare_sparse_attn_sharedkv(
     a.softmax_scale = float(softmax_scale)
     a.num_splits = int(num_splits)
     a.head_waves = int(head_waves)
+    a.waves = int(waves)
     return PreparedCall(a, keep, out, lse, layout_q, B, S_max)
 
 

@@ -6,23 +6,28 @@
 //
 //  1. Resolve the workgroup's slot range to physical cache rows through the
 //     block tables, drop masked slots (window band, idx < 0, idx >= causal
-//     threshold) and compact the survivors, in order, into LDS.
+//     threshold) and compact the survivors, in order, into LDS. The batch of
+//     the token comes from one ballot over q_prefix; the top-k indices, the
+//     batch scalars and the query load in one round trip, the block tables in
+//     a second one.
 //  2. The 4 waves form HW head-waves x KW key-groups (HW * KW = 4). A wave
 //     owns 16 query heads; a key-group owns a contiguous share of the rows and
-//     streams it in steps of 32 rows through an HW-deep ring of LDS slots.
-//     Rows move HBM -> LDS with global_load_lds_dwordx4 (no register staging,
-//     up to 4 x 36 KB in flight per CU), stored row-major with an XOR swizzle
-//     of 16-byte chunks so both operand reads below are bank-conflict free.
-//     fp8 rows go through registers instead (dequantised to bf16 on the way).
-//  3. Per step and wave:  S^T[32 keys x 16 heads] = K . Q^T  (16x16x32 MFMA,
+//     streams it in steps of TR rows (32, or 16 when every wave is its own
+//     key-group) through a ring of LDS slots. Rows move HBM -> LDS with
+//     global_load_lds_dwordx4 (no register staging), stored row-major with an
+//     XOR swizzle of 16-byte chunks so both operand reads below are
+//     bank-conflict free. fp8 rows go through registers instead (dequantised
+//     to bf16 on the way). With HW = 1 the waves share nothing until the
+//     epilogue, so the step loop has no workgroup barrier.
+//  3. Per step and wave:  S^T[TR keys x 16 heads] = K . Q^T  (16x16x32 MFMA,
 //     A from LDS, Q^T resident in VGPRs), sink-seeded online softmax in the
 //     log2 domain, P rounded to the query dtype, then
 //     O^T[512 x 16 heads] += V^T . P^T where the V^T operand comes straight
 //     from the row-major tile with ds_read_b64_tr_b16 and P^T is already in
 //     the register layout the MFMA wants (the S^T accumulator layout).
 //  4. Key-groups merge through LDS (max / sum rescale); the result is the
-//     output + LSE, or with several KV splits an unnormalised partial that
-//     the LSE combine kernel merges.
+//     output + LSE, or with several KV splits an unnormalised fp32 partial
+//     that the LSE combine kernel merges with the sink.
 //
 // Semantics follow sparse_attn_sharedkv_tilelang/kernel.py:254-277 (work
 // decode), :628-722 (window / compressed masks), :594-617 (sink seed),
@@ -31,6 +36,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdint>
 
@@ -41,14 +47,15 @@
 
 namespace {
 
-constexpr int kTR = 32;           // rows per pipeline step
 constexpr int kDV = 512;          // output / V channels
 constexpr int kMaxSlots = 1280;   // slot range one workgroup may own
+constexpr int kRoundsMax = kMaxSlots / 256;  // slot rounds at 256 threads
+constexpr int kMaxWaves = 8;
 constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dealt round-robin
-constexpr int kSplitTarget = 128; // workgroups the automatic split count aims for
+constexpr int kCus = 256;         // MI355X compute units (one forward workgroup each)
 constexpr int kRow656 = 656;      // fp8 cache row bytes
 constexpr int kChunksMax = 72;    // 16-byte chunks of a 576-channel bf16 row
-constexpr int kSlotChunks = kTR * kChunksMax;
+constexpr int kLdsRows = 128;     // rows of ring storage per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazyLog2 = 8.f;   // O / l rescale threshold (log2 units)
@@ -56,29 +63,13 @@ constexpr float kLazyLog2 = 8.f;   // O / l rescale threshold (log2 units)
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-// Four statically distinct LDS slots: the compiler tracks LDS-DMA writes per
-// buffer, so reads of one slot never wait on loads still landing in another.
-__shared__ __attribute__((aligned(16))) uint4 lds_slot0[kSlotChunks];
-__shared__ __attribute__((aligned(16))) uint4 lds_slot1[kSlotChunks];
-__shared__ __attribute__((aligned(16))) uint4 lds_slot2[kSlotChunks];
-__shared__ __attribute__((aligned(16))) uint4 lds_slot3[kSlotChunks];
+__shared__ __attribute__((aligned(16))) uint4 lds_ring[kLdsRows * kChunksMax];  // 147,456 B
 __shared__ int lds_rows[kMaxSlots];
-__shared__ int lds_cnt[8];
-__shared__ float lds_ml[4][2][16];
-
-__device__ __forceinline__ uint4* slot_by_index(int i) {
-  return i == 0 ? lds_slot0 : i == 1 ? lds_slot1 : i == 2 ? lds_slot2 : lds_slot3;
-}
-
-template <int S>
-__device__ __forceinline__ uint4* slot_ptr() {
-  if constexpr (S == 0) return lds_slot0;
-  else if constexpr (S == 1) return lds_slot1;
-  else if constexpr (S == 2) return lds_slot2;
-  else return lds_slot3;
-}
+__shared__ int lds_cnt[kRoundsMax][kMaxWaves];
+__shared__ float lds_ml[kMaxWaves][2][16];
 
 struct FwdParams {
   const uint8_t* q;
@@ -133,17 +124,31 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t v) {
   return (v & 0x80u) ? -f : f;
 }
 
+// 16x16x32: A = 8 values of row l%16 (k = 8*(l/16)..), B likewise by column
 template <typename QT>
-__device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, const f32x4& c);
+__device__ __forceinline__ f32x4 mfma32k(const uint4& a, const uint4& b, const f32x4& c);
 template <>
-__device__ __forceinline__ f32x4 mfma16<__bf16>(const uint4& a, const uint4& b, const f32x4& c) {
+__device__ __forceinline__ f32x4 mfma32k<__bf16>(const uint4& a, const uint4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 template <>
-__device__ __forceinline__ f32x4 mfma16<_Float16>(const uint4& a, const uint4& b, const f32x4& c) {
+__device__ __forceinline__ f32x4 mfma32k<_Float16>(const uint4& a, const uint4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+// 16x16x16: A = 4 values of row l%16 (k = 4*(l/16)..), B likewise by column
+template <typename QT>
+__device__ __forceinline__ f32x4 mfma16k(const uint2& a, const uint2& b, const f32x4& c);
+template <>
+__device__ __forceinline__ f32x4 mfma16k<__bf16>(const uint2& a, const uint2& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                   __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16k<_Float16>(const uint2& a, const uint2& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                               __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
 }
 
 // Chunk swizzle inside each aligned group of 8 chunks of a row: row r keeps
@@ -156,8 +161,8 @@ __device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 
 // as inline asm so the compiler does not track it: its LDS-DMA tracking
 // cannot tell the slots apart for transposed LDS reads and would wait for
 // every load in flight. Completion is ordered explicitly with wait_vm<>()
-// and lds_barrier(); loads return in order, so the compiler's own vmcnt
-// waits for its loads stay conservative.
+// (loads return in order, so the compiler's own vmcnt waits for its loads
+// stay conservative).
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
   asm volatile(
       "s_mov_b32 m0, %1\n\t"
@@ -178,10 +183,26 @@ __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 63] known only at run time
+__device__ __forceinline__ void wait_vm_rt(int n) {
+  switch (n) {
+#define SAS_WAITCASE(k) case k: wait_vm<k>(); break;
+#define SAS_WAITCASE8(k) SAS_WAITCASE(k) SAS_WAITCASE(k + 1) SAS_WAITCASE(k + 2) SAS_WAITCASE(k + 3) \
+    SAS_WAITCASE(k + 4) SAS_WAITCASE(k + 5) SAS_WAITCASE(k + 6) SAS_WAITCASE(k + 7)
+    SAS_WAITCASE8(0) SAS_WAITCASE8(8) SAS_WAITCASE8(16) SAS_WAITCASE8(24)
+    SAS_WAITCASE8(32) SAS_WAITCASE8(40) SAS_WAITCASE8(48) SAS_WAITCASE8(56)
+#undef SAS_WAITCASE8
+#undef SAS_WAITCASE
+    default: wait_vm<0>(); break;
+  }
+}
+__device__ __forceinline__ void wait_lgkm0() {
+  __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+}
 // LDS reads done, then a workgroup barrier (no memory fence: in-flight LDS
 // DMA of other slots keeps streaming across it).
 __device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+  wait_lgkm0();
   __builtin_amdgcn_s_barrier();
 }
 
@@ -189,74 +210,96 @@ __device__ __forceinline__ void lds_barrier() {
 // forward kernel
 // ---------------------------------------------------------------------------
 
-// HW head-waves x KW key-groups; D = q/k channels; QT = query dtype;
-// KVF: 0 = cache rows in the query dtype, 1 = 656-byte fp8 rows.
-template <int HW, int D, typename QT, int KVF>
+// NW waves = HW head-waves x CS channel-halves x KW key-groups; D = q/k
+// channels; QT = query dtype; KVF: 0 = cache rows in the query dtype,
+// 1 = 656-byte fp8 rows. With 8 waves (2 per SIMD, 256 registers each) a
+// wave holds the O of its 16 heads for half of the 512 V channels (CS = 2):
+// both halves compute the same S = QK^T, each accumulates its own channels.
+template <int HW, int NW, int D, typename QT, int KVF>
 struct Cfg {
-  static constexpr int KW = 4 / HW;
-  static constexpr int NST = HW;                 // ring depth per key-group
-  static constexpr int CH = D / 8;               // 16-byte chunks per bf16 row
-  static constexpr int KS = D / 32;              // QK^T k-steps
-  static constexpr int GT = HW * 64;             // threads per key-group
-  static constexpr int OPS = kTR * CH / GT;      // DMA ops per thread per step
+  static constexpr int CS = NW == 8 ? 2 : 1;
+  static constexpr int WK = HW * CS;                        // waves sharing a key-group's slots
+  static constexpr int KW = NW / WK;
+  static constexpr int NTL = kDV / 16 / CS;                 // 16-channel O tiles per wave
+  // rows per step: 32, or 16 when 32-row slots would leave a ring shallower than 2
+  static constexpr int TR = kLdsRows / (KW * 32) < 2 ? 16 : 32;
+  static constexpr int PFK = TR == 16 ? 4 : 3;              // K operand reads ahead
+  static constexpr int PFV = TR == 16 ? 8 : 4;              // V^T operand reads ahead
+  static constexpr bool CH2 = true;                         // two QK^T accumulation chains
+  static constexpr int MT = TR / 16;                        // 16-key tiles per step
+  static constexpr int NST = kLdsRows / (KW * TR);          // ring depth per key-group
+  static constexpr int SLOT = TR * kChunksMax;              // slot stride (chunks)
+  static constexpr int CH = D / 8;                          // 16-byte chunks per bf16 row
+  static constexpr int KS = D / 32;                         // QK^T k-steps
+  static constexpr int GT = WK * 64;                        // threads per key-group
+  static constexpr int NI = TR * CH / 64;                   // DMA instructions per step
+  static constexpr int OPS = (NI + WK - 1) / WK;            // most DMA ops per wave per step
   static constexpr int ROWB = KVF ? kRow656 : D * 2;
   // fp8 register staging: 40 work chunks per row (32 latent x 16 values, 8 rope)
   static constexpr int FCPR = 40;
-  static constexpr int FOPS = (kTR * FCPR + GT - 1) / GT;
-  static_assert(kTR * CH % GT == 0, "uniform DMA op count");
+  static constexpr int FOPS = (TR * FCPR + GT - 1) / GT;
+  static_assert(TR * CH % 64 == 0, "whole DMA instructions");
+  static_assert(NST >= 2 && NST <= 4, "ring depth");
+  static_assert((NST - 1) * OPS < 64, "vmcnt range");
+  static_assert(KW * NST * SLOT <= kLdsRows * kChunksMax, "ring fits");
 };
 
-template <int HW, int D, typename QT, int KVF>
+template <int HW, int NW, int D, typename QT, int KVF>
 struct Fwd {
-  using C = Cfg<HW, D, QT, KVF>;
+  using C = Cfg<HW, NW, D, QT, KVF>;
   const FwdParams& p;
-  const int lane, c16, g, kw, hw, gt;
-  const int* rows;     // this key-group's compacted row ids
+  const int lane, c16, g, kw, hw, cs, jw, gt, nops;
+  int rbeg;            // this key-group's first row in lds_rows
+  int ring;           // chunk offset of this key-group's NST slots in lds_ring
   int nrows;           // rows this key-group owns
   int nsteps, nsteps_max, dummy;
   uint4 qf[C::KS];
   float m_run, l_run;
-  f32x4 acc[kDV / 16];
+  f32x4 acc[C::NTL];
   uint4 fbuf[KVF ? C::FOPS : 1];
   float fsc[KVF ? C::FOPS : 1];
 
+  // wave = kw * WK + jw, jw = cs * HW + hw; wave jw of a key-group issues the
+  // DMA instructions i = jw, jw + WK, ... of every step (nops of them)
   __device__ Fwd(const FwdParams& p_, int lane_, int wave)
-      : p(p_), lane(lane_), c16(lane_ & 15), g(lane_ >> 4), kw(wave / HW), hw(wave % HW),
-        gt((wave % HW) * 64 + lane_) {}
+      : p(p_), lane(lane_), c16(lane_ & 15), g(lane_ >> 4), kw(wave / C::WK), hw(wave % HW),
+        cs((wave % C::WK) / HW), jw(wave % C::WK), gt((wave % C::WK) * 64 + lane_),
+        nops((C::NI - wave % C::WK + C::WK - 1) / C::WK) {}
 
   __device__ __forceinline__ const uint8_t* row_ptr(int id) const {
     return id >= 0 ? p.ori_kv + (size_t)id * C::ROWB : p.cmp_kv + (size_t)(-id - 2) * C::ROWB;
   }
+  __device__ __forceinline__ int slot(int j) const { return ring + j * C::SLOT; }
 
-  // -- bf16 / fp16 rows: DMA one 32-row step into slot SLOT --------------------
-  template <int SLOT>
-  __device__ __forceinline__ void issue(int step) {
-    uint4* slot = slot_ptr<SLOT>();
-    const int* rp = rows + step * kTR;
-    const int nk = min(kTR, nrows - step * kTR);
+  // -- bf16 / fp16 rows: DMA one step into slot j ------------------------------
+  __device__ __forceinline__ void issue(int j, int step) {
+    const int sl = slot(j);
+    const int rp = rbeg + step * C::TR;
+    const int nk = min(C::TR, nrows - step * C::TR);
 #pragma unroll
-    for (int j = 0; j < C::OPS; ++j) {
-      const int blk = j * C::GT + hw * 64;          // wave-uniform chunk base
+    for (int o = 0; o < C::OPS; ++o) {
+      if (C::NI % C::WK && o * C::WK + jw >= C::NI) break;   // wave-uniform
+      const int blk = (o * C::WK + jw) * 64;        // wave-uniform chunk base
       const int P = blk + lane;
       const int r = P / C::CH, pc = P - r * C::CH;
       const int c = pc ^ swz(r);
-      const int id = r < nk ? rp[r] : dummy;
-      dma16(row_ptr(id) + c * 16, __builtin_amdgcn_readfirstlane(lds_addr_of(slot + blk)));
+      const int id = r < nk ? lds_rows[rp + r] : dummy;
+      dma16(row_ptr(id) + c * 16, __builtin_amdgcn_readfirstlane(lds_addr_of(&lds_ring[sl + blk])));
     }
   }
 
-  // -- fp8 rows: global -> registers, dequantised into slot on store ---------
+  // -- fp8 rows: global -> registers, dequantised into a slot on store -------
   __device__ __forceinline__ void fload(int step) {
-    const int* rp = rows + step * kTR;
-    const int nk = min(kTR, nrows - step * kTR);
+    const int rp = rbeg + step * C::TR;
+    const int nk = min(C::TR, nrows - step * C::TR);
 #pragma unroll
     for (int k = 0; k < C::FOPS; ++k) {
       const int e = gt + k * C::GT;
       const int r = e / C::FCPR, c = e - r * C::FCPR;
       fbuf[k] = make_uint4(0, 0, 0, 0);
       fsc[k] = 0.f;
-      if (e < kTR * C::FCPR && r < nk) {
-        const uint8_t* src = row_ptr(rp[r]);
+      if (e < C::TR * C::FCPR && r < nk) {
+        const uint8_t* src = row_ptr(lds_rows[rp + r]);
         if (c < 32) {
           fbuf[k] = *reinterpret_cast<const uint4*>(src + c * 16);
           fsc[k] = *reinterpret_cast<const float*>(src + 512 + 4 * (c >> 3));
@@ -266,15 +309,14 @@ struct Fwd {
       }
     }
   }
-  template <int SLOT>
-  __device__ __forceinline__ void fstore() {
-    uint4* slot = slot_ptr<SLOT>();
+  __device__ __forceinline__ void fstore(int j) {
+    const int sl = slot(j);
 #pragma unroll
     for (int k = 0; k < C::FOPS; ++k) {
       const int e = gt + k * C::GT;
-      if (e >= kTR * C::FCPR) continue;
+      if (e >= C::TR * C::FCPR) continue;
       const int r = e / C::FCPR, c = e - r * C::FCPR;
-      uint4* row = slot + r * C::CH;
+      uint4* row = &lds_ring[sl + r * C::CH];
       const int sw = swz(r);
       if (c < 32) {
         const uint32_t w[4] = {fbuf[k].x, fbuf[k].y, fbuf[k].z, fbuf[k].w};
@@ -294,55 +336,59 @@ struct Fwd {
     }
   }
 
-  // -- one 32-key step of attention for this wave's 16 heads ----------------
-  template <int SLOT>
-  __device__ __forceinline__ void compute(int step) {
-    const uint4* slot = slot_ptr<SLOT>();
-    const int nk = min(kTR, nrows - step * kTR);
-    f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  // -- one step of attention (TR keys) for this wave's 16 heads --------------
+  __device__ __forceinline__ void compute(int sl, int step) {
+    constexpr int MT = C::MT;
+    const int nk = min(C::TR, nrows - step * C::TR);
+    f32x4 sacc[MT], sodd[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) { sacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f}; sodd[mt] = sacc[mt]; }
     // K operand: rows c16 and 16 + c16 share swz(); logical chunk 4ks + g only
     // changes in its low 3 bits with ks & 1, the rest is an immediate offset.
     // Reads run kPfK k-steps ahead of the MFMAs that consume them.
     const int ksw = swz(c16);
-    const uint4* qrow = slot + c16 * C::CH;
+    const uint4* qrow = &lds_ring[sl + c16 * C::CH];
     const int qo0 = g ^ ksw, qo1 = (4 + g) ^ ksw;
     auto kfrag = [&](int ks, int mt) {
       return qrow[mt * 16 * C::CH + (ks >> 1) * 8 + ((ks & 1) ? qo1 : qo0)];
     };
-    constexpr int kPfK = 3;
-    uint4 af[kPfK][2];
+    constexpr int kPfK = C::PFK;
+    uint4 af[kPfK][MT];
 #pragma unroll
-    for (int i = 0; i < kPfK; ++i) { af[i][0] = kfrag(i, 0); af[i][1] = kfrag(i, 1); }
-    // even / odd k-steps accumulate separately: four independent MFMA chains
-    f32x4 sodd[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    for (int i = 0; i < kPfK; ++i)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) af[i][mt] = kfrag(i, mt);
+    // even / odd k-steps accumulate separately: 2 MT independent MFMA chains
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
-      const uint4 a0 = af[ks % kPfK][0], a1 = af[ks % kPfK][1];
+      uint4 a[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) a[mt] = af[ks % kPfK][mt];
       if (ks + kPfK < C::KS) {
-        af[ks % kPfK][0] = kfrag(ks + kPfK, 0);
-        af[ks % kPfK][1] = kfrag(ks + kPfK, 1);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) af[ks % kPfK][mt] = kfrag(ks + kPfK, mt);
       }
-      if (ks & 1) {
-        sodd[0] = mfma16<QT>(a0, qf[ks], sodd[0]);
-        sodd[1] = mfma16<QT>(a1, qf[ks], sodd[1]);
-      } else {
-        sacc[0] = mfma16<QT>(a0, qf[ks], sacc[0]);
-        sacc[1] = mfma16<QT>(a1, qf[ks], sacc[1]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (C::CH2 && (ks & 1)) sodd[mt] = mfma32k<QT>(a[mt], qf[ks], sodd[mt]);
+        else sacc[mt] = mfma32k<QT>(a[mt], qf[ks], sacc[mt]);
       }
     }
-    // schedule: the prefetch reads first, then per k-step 2 MFMAs + 2 reads
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPfK, 0);
+    // schedule: the prefetch reads first, then per k-step MT MFMAs + MT reads
+    __builtin_amdgcn_sched_group_barrier(0x100, MT * kPfK, 0);
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      if (ks + kPfK < C::KS) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, MT, 0);
+      if (ks + kPfK < C::KS) __builtin_amdgcn_sched_group_barrier(0x100, MT, 0);
     }
-    sacc[0] += sodd[0];
-    sacc[1] += sodd[1];
-    float sv[2][4];
+    if constexpr (C::CH2) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) sacc[mt] += sodd[mt];
+    }
+    float sv[MT][4];
     float mloc = -INFINITY;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int key = mt * 16 + g * 4 + j;
@@ -361,12 +407,12 @@ struct Fwd {
       l_run *= alpha;
       m_run = m_new;
 #pragma unroll
-      for (int mt = 0; mt < kDV / 16; ++mt) acc[mt] *= alpha;
+      for (int i = 0; i < C::NTL; ++i) acc[i] *= alpha;
     }
     float lsum = 0.f;
-    uint32_t pk[4];
+    uint32_t pk[2 * MT];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       float pv[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -379,203 +425,440 @@ struct Fwd {
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
     l_run += lsum;
-    const uint4 pfrag = make_uint4(pk[0], pk[1], pk[2], pk[3]);
     // V^T operand by transposed reads: lanes of group g address rows
     // 4g + c16/4 (and +16), channels mt*16 + 4*(c16&3); each lane receives
     // 4 keys of channel mt*16 + c16. Reads run kPfV channel tiles ahead.
+    // This wave's O tiles are channel tiles cs * NTL + mt, mt < NTL (their
+    // chunks start cs * NTL * 2 chunks into the row).
     const int vr = 4 * g + (c16 >> 2);
     const int vsw = swz(vr);
     const int vb = (c16 & 3) >> 1;
-    const char* vbase = reinterpret_cast<const char*>(slot) + vr * C::CH * 16 + (c16 & 1) * 8;
+    const char* vbase = reinterpret_cast<const char*>(&lds_ring[sl + vr * C::CH]) + (c16 & 1) * 8 +
+                        cs * (C::NTL / 4) * 128;
     // logical chunk 2mt + vb: its low 3 bits cycle with mt & 3
     int voff[4];
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) voff[q4] = ((2 * q4 + vb) ^ vsw) * 16;
-    auto vfrag = [&](int mt) {
-      const char* a0 = vbase + (mt >> 2) * 128 + voff[mt & 3];
-      const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a0));
-      const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a0 + 16 * C::CH * 16));
-      const uint2 u0 = __builtin_bit_cast(uint2, v0), u1 = __builtin_bit_cast(uint2, v1);
-      return make_uint4(u0.x, u0.y, u1.x, u1.y);
-    };
-    constexpr int kPfV = 4;
-    uint4 vf[kPfV];
+    constexpr int kPfV = C::PFV;
+    if constexpr (MT == 2) {
+      auto vfrag = [&](int mt) {
+        const char* a0 = vbase + (mt >> 2) * 128 + voff[mt & 3];
+        const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a0));
+        const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a0 + 16 * C::CH * 16));
+        const uint2 u0 = __builtin_bit_cast(uint2, v0), u1 = __builtin_bit_cast(uint2, v1);
+        return make_uint4(u0.x, u0.y, u1.x, u1.y);
+      };
+      const uint4 pfrag = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      uint4 vf[kPfV];
 #pragma unroll
-    for (int i = 0; i < kPfV; ++i) vf[i] = vfrag(i);
+      for (int i = 0; i < kPfV; ++i) vf[i] = vfrag(i);
 #pragma unroll
-    for (int mt = 0; mt < kDV / 16; ++mt) {
-      const uint4 a = vf[mt % kPfV];
-      if (mt + kPfV < kDV / 16) vf[mt % kPfV] = vfrag(mt + kPfV);
-      acc[mt] = mfma16<QT>(a, pfrag, acc[mt]);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPfV, 1);
+      for (int mt = 0; mt < C::NTL; ++mt) {
+        const uint4 a = vf[mt % kPfV];
+        if (mt + kPfV < C::NTL) vf[mt % kPfV] = vfrag(mt + kPfV);
+        acc[mt] = mfma32k<QT>(a, pfrag, acc[mt]);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPfV, 1);
 #pragma unroll
-    for (int mt = 0; mt < kDV / 16; ++mt) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      if (mt + kPfV < kDV / 16) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      for (int mt = 0; mt < C::NTL; ++mt) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        if (mt + kPfV < C::NTL) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      }
+    } else {
+      // 16 keys: one transposed read per 16-channel tile, 16x16x16 MFMA whose
+      // B operand (keys 4g..4g+3 of head c16) is exactly this lane's P
+      auto vfrag = [&](int mt) {
+        const char* a0 = vbase + (mt >> 2) * 128 + voff[mt & 3];
+        return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a0)));
+      };
+      const uint2 pfrag = make_uint2(pk[0], pk[1]);
+      constexpr int kPf = C::PFV;
+      uint2 vf[kPf];
+#pragma unroll
+      for (int i = 0; i < kPf; ++i) vf[i] = vfrag(i);
+#pragma unroll
+      for (int mt = 0; mt < C::NTL; ++mt) {
+        const uint2 a = vf[mt % kPf];
+        if (mt + kPf < C::NTL) vf[mt % kPf] = vfrag(mt + kPf);
+        acc[mt] = mfma16k<QT>(a, pfrag, acc[mt]);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, kPf, 1);
+#pragma unroll
+      for (int mt = 0; mt < C::NTL; ++mt) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        if (mt + kPf < C::NTL) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      }
     }
   }
 
-  // -- the step loop of key-group KWI (slots KWI*NST .. +NST-1) ---------------
-  template <int KWI, int J>
+  // Step sync. WK > 1: the key-group's waves share slots, so a workgroup
+  // barrier; WK = 1: the wave reads only slots it filled itself, and its own
+  // LDS-DMA writes are complete once vmcnt has drained past them.
+  __device__ __forceinline__ void step_sync() {
+    if constexpr (C::WK > 1) lds_barrier();
+    else wait_lgkm0();
+  }
+
+  // -- the step loop of this key-group ----------------------------------------
+  template <int J>
   __device__ __forceinline__ void step_j(int it0) {
-    constexpr int SLOT = KWI * C::NST + J;
     const int it = it0 + J;
-    if (it >= nsteps_max) return;                       // uniform over the workgroup
+    if (it >= nsteps_max) return;   // uniform over the workgroup (HW > 1) / wave
     if constexpr (!KVF) {
       // my DMA for step `it` done (steps after it may still stream), then all waves
       const int after = it < nsteps ? min(C::NST - 1, nsteps - 1 - it) : 0;
-      if (after <= 0) wait_vm<0>();
-      else if (after == 1) wait_vm<C::OPS>();
-      else if (after == 2) wait_vm<(C::NST > 2 ? 2 * C::OPS : 0)>();
-      else wait_vm<(C::NST > 3 ? 3 * C::OPS : 0)>();
-      lds_barrier();
-      if (it < nsteps) compute<SLOT>(it);
-      lds_barrier();
-      if (it + C::NST < nsteps) issue<SLOT>(it + C::NST);
-    } else {
-      // fp8: registers hold step it+1; slot (it & 1) of the group holds step it
-      lds_barrier();
-      if (it < nsteps) compute<SLOT>(it);
-      if (it + 1 < nsteps) {
-        constexpr int NEXT = KWI * C::NST + ((J + 1) % C::NST);
-        fstore<NEXT>();
+      if constexpr (C::NI % C::WK) {
+        wait_vm_rt(max(after, 0) * nops);
+      } else {
+        if (after <= 0) wait_vm<0>();
+        else if (after == 1) wait_vm<C::OPS>();
+        else if (after == 2) wait_vm<(C::NST > 2 ? 2 * C::OPS : 0)>();
+        else wait_vm<(C::NST > 3 ? 3 * C::OPS : 0)>();
       }
+      step_sync();
+      if (it < nsteps) compute(slot(J), it);
+      step_sync();
+      if (it + C::NST < nsteps) issue(J, it + C::NST);
+    } else {
+      // fp8: registers hold step it+1; slot J holds step it
+      step_sync();
+      if (it < nsteps) compute(slot(J), it);
+      if (it + 1 < nsteps) fstore((J + 1) % C::NST);
       if (it + 2 < nsteps) fload(it + 2);
     }
   }
 
-  template <int KWI>
-  __device__ __forceinline__ void run_group() {
+  __device__ __forceinline__ void run() {
     if constexpr (!KVF) {
 #pragma unroll
-      for (int j = 0; j < C::NST; ++j) {
-        if (j < nsteps) {
-          if (j == 0) issue<KWI * C::NST + 0>(0);
-          if constexpr (C::NST > 1) if (j == 1) issue<KWI * C::NST + 1>(1);
-          if constexpr (C::NST > 2) if (j == 2) issue<KWI * C::NST + 2>(2);
-          if constexpr (C::NST > 3) if (j == 3) issue<KWI * C::NST + 3>(3);
-        }
-      }
+      for (int j = 0; j < C::NST; ++j)
+        if (j < nsteps) issue(j, j);
     } else {
-      if (nsteps > 0) { fload(0); fstore<KWI * C::NST>(); }
+      if (nsteps > 0) { fload(0); fstore(0); }
       if (nsteps > 1) fload(1);
     }
     for (int it0 = 0; it0 < nsteps_max; it0 += C::NST) {
-      step_j<KWI, 0>(it0);
-      if constexpr (C::NST > 1) step_j<KWI, 1>(it0);
-      if constexpr (C::NST > 2) step_j<KWI, 2>(it0);
-      if constexpr (C::NST > 3) step_j<KWI, 3>(it0);
+      step_j<0>(it0);
+      step_j<1>(it0);
+      if constexpr (C::NST > 2) step_j<2>(it0);
+      if constexpr (C::NST > 3) step_j<3>(it0);
     }
   }
 };
 
-template <int HW, int D, typename QT, int KVF>
-__global__ void __launch_bounds__(256)
-sas_fwd_kernel(const FwdParams p) {
-  using C = Cfg<HW, D, QT, KVF>;
-  static_assert(!KVF || HW >= 2, "fp8 staging needs a ring of at least 2 slots");
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+template <typename QT>
+__device__ __forceinline__ void store_out4(const FwdParams& p, int t, int h, int c4, float4 o, float inv) {
+  const uint32_t w0 = to_bits<QT>(o.x * inv) | (to_bits<QT>(o.y * inv) << 16);
+  const uint32_t w1 = to_bits<QT>(o.z * inv) | (to_bits<QT>(o.w * inv) << 16);
+  *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + ((size_t)t * p.H + h) * kDV + c4 * 4) =
+      make_uint2(w0, w1);
+}
 
+// Merge the nsplit fp32 partials of (token t, heads [h0, h0 + nh)) with the
+// sink into out / lse: M = max(sink, m_i), L = 2^(sink-M) + sum_i l_i
+// 2^(m_i-M), out = sum_i 2^(m_i-M) O_i / L, lse = (M ln 2) + ln L (a running
+// merge over i, kB splits' loads in flight together). A negative l marks a
+// padded token (out = 0, lse = 0).
+template <typename QT>
+__device__ __forceinline__ void merge_partials(const FwdParams& p, int t, int h0, int nh, int tid,
+                                               int nthreads) {
+  constexpr int kB = 4;
+  const int S = p.nsplit;
+  const float* po = p.part_o + (size_t)t * S * p.H * kDV;
+  const float* pm = p.part_ml + (size_t)t * S * p.H * 2;
+  for (int e = tid; e < nh * (kDV / 4); e += nthreads) {
+    const int h = h0 + e / (kDV / 4), c4 = e % (kDV / 4);
+    float M = p.sinks[h] * kLog2e, L = 1.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    bool pad = false;
+    for (int s0 = 0; s0 < S; s0 += kB) {
+      float2 ml[kB];
+      float4 v[kB];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const size_t row = (size_t)min(s0 + j, S - 1) * p.H + h;
+        ml[j] = *reinterpret_cast<const float2*>(pm + row * 2);
+        v[j] = *reinterpret_cast<const float4*>(po + row * kDV + c4 * 4);
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        if (s0 + j >= S) break;
+        pad |= ml[j].y < 0.f;
+        if (ml[j].x > M) {
+          const float a = exp2f(M - ml[j].x);
+          L *= a; o.x *= a; o.y *= a; o.z *= a; o.w *= a;
+          M = ml[j].x;
+        }
+        const float w = ml[j].x == -INFINITY ? 0.f : exp2f(ml[j].x - M);
+        L += w * ml[j].y;
+        o.x += w * v[j].x; o.y += w * v[j].y; o.z += w * v[j].z; o.w += w * v[j].w;
+      }
+    }
+    store_out4<QT>(p, t, h, c4, o, pad ? 0.f : 1.f / L);
+    if (c4 == 0) p.lse[(size_t)t * p.H + h] = pad ? 0.f : M * kLn2 + logf(L);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// shared prologue: slot resolution
+// ---------------------------------------------------------------------------
+
+struct Tok {
+  int t, hg, sp;     // token, head group, KV split
+  int b, nvalid;     // batch, compacted rows in lds_rows
+  bool padded;       // (b, position) outside the batch's query length
+};
+
+__device__ __forceinline__ Tok item_of(const FwdParams& p) {
   // XCD-aware item mapping: XCD x = blockIdx % 8 owns a contiguous item range,
   // so all splits / head groups of a token (and neighbouring tokens) share L2.
   const int item = (int)(blockIdx.x % kXcds) * p.per_xcd + (int)(blockIdx.x / kXcds);
-  if (item >= p.items) return;
+  Tok k;
   const int per_tok = p.nhg * p.nsplit;
-  const int t = item / per_tok;
-  const int hg = (item % per_tok) / p.nsplit;
-  const int sp = item % p.nsplit;
+  k.t = item / per_tok;
+  k.hg = (item % per_tok) / p.nsplit;
+  k.sp = item % p.nsplit;
+  k.b = 0; k.nvalid = 0; k.padded = true;
+  return k;
+}
 
-  // token -> (batch, position): largest b with q_prefix[b] <= t
-  int lo = 0, hi = p.B - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.q_prefix[mid] <= t) lo = mid; else hi = mid - 1;
-  }
-  const int b = lo;
-  const int s = t - p.q_prefix[b];
-  const int aq = p.act_q[b], akv = p.act_kv[b];
-  const bool padded = s < 0 || s >= aq;
-  const int sg = akv - aq + s;                               // causal position
-  const int nwin = (padded || sg < 0) ? 0 : min(sg, p.win_left) + 1;
-  const int wlo = sg - nwin + 1;                             // = max(sg - win_left, 0)
-  const int thr = (padded || sg + 1 <= 0) ? 0 : (sg + 1) / p.cmp_ratio;
+// Resolve the item's slot range to cache rows and compact the valid ones, in
+// slot order, into lds_rows[0, nvalid). Raw rows are stored as id >= 0,
+// compressed rows as -(id + 2). `mid` runs after the block-table loads are
+// issued (a caller can put its own loads behind them there).
+template <int NT, typename Mid>
+__device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int lane, int wave, Mid&& mid) {
+  constexpr int NWV = NT / 64;
+  constexpr int kRounds = (kMaxSlots + NT - 1) / NT;
+  static_assert(kRounds <= kRoundsMax && NWV <= kMaxWaves, "resolve geometry");
+  const int t = k.t;
   const int wincap = p.win_left + 1;
-  const int nslots = wincap + (p.scenario >= 2 ? p.K : 0);
-  const int s0 = sp * p.slots_per_split;
+  const int nslots = wincap + (p.scenario >= SAS_CFA ? p.K : 0);
+  const int s0 = k.sp * p.slots_per_split;
   const int s1 = min(s0 + p.slots_per_split, nslots);
+  const int nr = (s1 - s0 + NT - 1) / NT;   // slot rounds of NT (<= kRounds)
 
-  // The first slot chunk's top-k index is fetched before Q (loads return in
-  // order, so waiting for the index never waits for Q); Q's latency then
-  // overlaps the block-table lookups of the slot resolution.
-  int idx_first = 0;
-  {
-    const int j = s0 + tid;
-    if (p.scenario == SAS_SCFA && j < s1 && j >= wincap && !padded)
-      idx_first = p.cmp_idx[(size_t)t * p.K + (j - wincap)];
-  }
-  // Q^T operand in registers (head hq, channels ks*32 + 8g .. +8)
-  Fwd<HW, D, QT, KVF> f(p, lane, wave);
-  const int hq = hg * (16 * HW) + f.hw * 16 + f.c16;
-  {
-    const uint4* qp = reinterpret_cast<const uint4*>(p.q + ((size_t)t * p.H + hq) * D * 2);
+  // ---- round trip 1: top-k indices and batch scalars ------------------------
+  int idxv[kRounds];
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) f.qf[ks] = qp[ks * 4 + f.g];
+  for (int r = 0; r < kRounds; ++r) {
+    idxv[r] = -1;
+    const int j = s0 + r * NT + tid;
+    if (r < nr && p.scenario == SAS_SCFA && j < s1 && j >= wincap)
+      idxv[r] = p.cmp_idx[(size_t)t * p.K + (j - wincap)];
   }
+  int qp0 = INT_MAX, aq0 = 0, akv0 = 0;
+  if (lane < p.B) { qp0 = p.q_prefix[lane]; aq0 = p.act_q[lane]; akv0 = p.act_kv[lane]; }
+  // token -> (batch, position): largest b with q_prefix[b] <= t (q_prefix is
+  // non-decreasing), one ballot per 64 batches
+  int b = 0, aq = 0, akv = 0, qpb = 0;
+  {
+    uint64_t m = __ballot(qp0 <= t);
+    int n = __popcll(m);
+    if (n) { b = n - 1; qpb = __shfl(qp0, n - 1); aq = __shfl(aq0, n - 1); akv = __shfl(akv0, n - 1); }
+    for (int c = 64; n == 64 && c < p.B; c += 64) {
+      const int i = c + lane;
+      int qpi = INT_MAX, aqi = 0, akvi = 0;
+      if (i < p.B) { qpi = p.q_prefix[i]; aqi = p.act_q[i]; akvi = p.act_kv[i]; }
+      m = __ballot(qpi <= t);
+      n = __popcll(m);
+      if (n) { b = c + n - 1; qpb = __shfl(qpi, n - 1); aq = __shfl(aqi, n - 1); akv = __shfl(akvi, n - 1); }
+    }
+  }
+  const int spos = t - qpb;
+  const bool padded = spos < 0 || spos >= aq;
+  const int sg = akv - aq + spos;                              // causal position
+  const int nwin = (padded || sg < 0) ? 0 : min(sg, p.win_left) + 1;
+  const int wlo = sg - nwin + 1;                               // = max(sg - win_left, 0)
+  const int thr = (padded || sg + 1 <= 0) ? 0 : (sg + 1) / p.cmp_ratio;
 
-  // ---- 1. resolve + compact slot range [s0, s1) -------------------------
-  // Stored ids: raw rows as id >= 0, compressed rows as -(id + 2).
-  int nvalid = 0;
-  for (int c0 = s0; c0 < s1; c0 += 256) {
-    const int j = c0 + tid;
-    int rid = -1;
-    if (j < s1 && !padded) {
+  // ---- round trip 2: block tables -------------------------------------------
+  // Every table read is issued unconditionally at a clamped, in-range
+  // address (validity is kept apart), so the reads of all rounds are in
+  // flight together and retire with one wait.
+  int rid[kRounds];
+  {
+    const int32_t* obt = p.ori_bt + (size_t)b * p.ori_bt_stride;
+    const int32_t* cbt = p.cmp_bt ? p.cmp_bt + (size_t)b * p.cmp_bt_stride : obt;
+    int phys[kRounds], off[kRounds];
+    bool ok[kRounds], ori[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      phys[r] = -1; ok[r] = false; ori[r] = true; off[r] = 0;
+      if (r >= nr) continue;   // uniform
+      const int j = s0 + r * NT + tid;
+      const bool live = j < s1 && !padded;
+      int blk;
       if (j < wincap) {
-        if (j < nwin) {
-          const int pos = wlo + j;
-          const int blk = pos / p.ori_bs;
-          if (blk < p.ori_bt_stride) {
-            const int phys = p.ori_bt[(size_t)b * p.ori_bt_stride + blk];
-            if (phys >= 0 && phys < p.ori_nblocks) rid = phys * p.ori_bs + pos % p.ori_bs;
-          }
-        }
+        const int pos = wlo + j;
+        blk = pos / p.ori_bs;
+        off[r] = pos - blk * p.ori_bs;
+        ok[r] = live && j < nwin && blk < p.ori_bt_stride;
       } else {
-        const int k = j - wincap;
-        const int idx = p.scenario != SAS_SCFA ? k
-                        : c0 == s0 ? idx_first : p.cmp_idx[(size_t)t * p.K + k];
-        if (idx >= 0 && idx < thr) {
-          const int blk = idx / p.cmp_bs;
-          if (blk < p.cmp_bt_stride) {
-            const int phys = p.cmp_bt[(size_t)b * p.cmp_bt_stride + blk];
-            if (phys >= 0 && phys < p.cmp_nblocks) rid = -(phys * p.cmp_bs + idx % p.cmp_bs + 2);
-          }
-        }
+        const int idx = p.scenario == SAS_SCFA ? idxv[r] : j - wincap;
+        const int ic = max(idx, 0);
+        blk = ic / p.cmp_bs;
+        off[r] = ic - blk * p.cmp_bs;
+        ori[r] = false;
+        ok[r] = live && idx >= 0 && idx < thr && blk < p.cmp_bt_stride;
+      }
+      phys[r] = (ori[r] ? obt : cbt)[ok[r] ? blk : 0];
+    }
+    // the caller's loads go behind the table reads, so waiting for the
+    // tables leaves them in flight
+    asm volatile("" ::: "memory");
+    mid();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      rid[r] = -1;
+      if (ori[r]) {
+        if (ok[r] && phys[r] >= 0 && phys[r] < p.ori_nblocks) rid[r] = phys[r] * p.ori_bs + off[r];
+      } else {
+        if (ok[r] && phys[r] >= 0 && phys[r] < p.cmp_nblocks) rid[r] = -(phys[r] * p.cmp_bs + off[r] + 2);
       }
     }
-    const bool v = rid != -1;
-    const uint64_t mask = __ballot(v);
-    const int before = __popcll(mask & ((1ull << lane) - 1ull));
-    if (lane == 0) lds_cnt[wave] = __popcll(mask);
-    lds_barrier();
+  }
+  // ---- compaction (ballot + per-wave counts) -------------------------------
+  uint64_t vmask[kRounds];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    vmask[r] = __ballot(rid[r] != -1);
+    if (r < nr && lane == 0) lds_cnt[r][wave] = __popcll(vmask[r]);
+  }
+  __syncthreads();
+  int nvalid = 0;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    if (r >= nr) break;
     int wpre = 0, tot = 0;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const int cw = lds_cnt[w];
+    for (int w = 0; w < NWV; ++w) {
+      const int cw = lds_cnt[r][w];
       wpre += w < wave ? cw : 0;
       tot += cw;
     }
-    if (v) lds_rows[nvalid + wpre + before] = rid;
+    if (rid[r] != -1)
+      lds_rows[nvalid + wpre + __popcll(vmask[r] & ((1ull << lane) - 1ull))] = rid[r];
     nvalid += tot;
-    lds_barrier();
   }
+  __syncthreads();
+  k.b = b;
+  k.nvalid = nvalid;
+  k.padded = padded;
+}
 
-  // key-group shares: whole 32-row steps, group 0 first
-  const int per = ((nvalid + C::KW * kTR - 1) / (C::KW * kTR)) * kTR;
+// ---------------------------------------------------------------------------
+// shared epilogue
+// ---------------------------------------------------------------------------
+
+constexpr int kObufStride = kDV + 4;   // floats per staged head row (bank spread)
+constexpr int kObufChunks = 16 * kObufStride / 4;   // one wave's 16 staged head rows
+static_assert(kMaxWaves / 2 * kObufChunks <= kLdsRows * kChunksMax, "epilogue staging fits");
+
+// After the step loop every wave holds (m, l, acc) of its 16 heads over its
+// key-group's rows. The KW key-groups of each head-wave are rescaled to a
+// common max and summed pairwise through LDS (a tree: half of the remaining
+// waves stage their O, the other half add it), then the key-group-0 waves
+// write the output (one split) or the split's fp32 partial (merged by the
+// split-KV combine kernel).
+template <int HW, int NW, int CS, typename QT>
+__device__ __forceinline__ void epilogue(const FwdParams& p, const Tok& k, int tid, int wave, int lane,
+                                         float m_run, float l_run, f32x4 (&acc)[kDV / 16 / CS]) {
+  constexpr int WK = HW * CS, KW = NW / WK, NTL = kDV / 16 / CS;
+  const int c16 = lane & 15, g = lane >> 4, kw = wave / WK, jw = wave % WK, hw = jw % HW, cs = jw / HW;
+  const int ch0 = cs * NTL * 16;   // this wave's first O channel
+  const int nhead_wg = 16 * HW;
+  const int hq = k.hg * nhead_wg + hw * 16 + c16;
+  const bool split = p.nsplit > 1;
+  const int t = k.t;
+  float M = m_run, L = l_run;
+  if constexpr (KW > 1) {
+    if (g == 0) { lds_ml[wave][0][c16] = m_run; lds_ml[wave][1][c16] = l_run; }
+    __syncthreads();
+    M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < KW; ++j) M = fmaxf(M, lds_ml[j * WK + jw][0][c16]);
+    L = 0.f;
+    float w_self = 0.f;
+#pragma unroll
+    for (int j = 0; j < KW; ++j) {
+      const float mk = lds_ml[j * WK + jw][0][c16];
+      const float wk = mk == -INFINITY ? 0.f : exp2f(mk - M);
+      L += wk * lds_ml[j * WK + jw][1][c16];
+      if (j == kw) w_self = wk;
+    }
+#pragma unroll
+    for (int mt = 0; mt < NTL; ++mt) acc[mt] *= w_self;
+#pragma unroll
+    for (int half = KW / 2; half >= 1; half >>= 1) {
+      if (kw >= half && kw < 2 * half) {
+        float* ob = reinterpret_cast<float*>(lds_ring + ((kw - half) * WK + jw) * kObufChunks);
+#pragma unroll
+        for (int mt = 0; mt < NTL; ++mt)
+          *reinterpret_cast<f32x4*>(ob + c16 * kObufStride + mt * 16 + g * 4) = acc[mt];
+      }
+      __syncthreads();
+      if (kw < half) {
+        const float* ob = reinterpret_cast<const float*>(lds_ring + (kw * WK + jw) * kObufChunks);
+#pragma unroll
+        for (int mt = 0; mt < NTL; ++mt)
+          acc[mt] += *reinterpret_cast<const f32x4*>(ob + c16 * kObufStride + mt * 16 + g * 4);
+      }
+      __syncthreads();
+    }
+  }
+  if (kw == 0) {
+    if (!split) {
+      const float inv = k.padded ? 0.f : 1.f / L;
+#pragma unroll
+      for (int mt = 0; mt < NTL; ++mt)
+        store_out4<QT>(p, t, hq, (ch0 >> 2) + mt * 4 + g,
+                       make_float4(acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]), inv);
+      if (g == 0 && cs == 0) p.lse[(size_t)t * p.H + hq] = k.padded ? 0.f : M * kLn2 + logf(L);
+    } else {
+      const size_t row = ((size_t)t * p.nsplit + k.sp) * p.H + hq;
+      float* po = p.part_o + row * kDV + ch0;
+#pragma unroll
+      for (int mt = 0; mt < NTL; ++mt)
+        *reinterpret_cast<f32x4*>(po + mt * 16 + g * 4) = acc[mt];
+      if (g == 0 && cs == 0)   // l < 0 marks a padded token
+        *reinterpret_cast<float2*>(p.part_ml + row * 2) = make_float2(M, k.padded ? -1.f : L);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// forward kernel, head-waves sharing LDS tiles (HW = 2, 4)
+// ---------------------------------------------------------------------------
+
+template <int HW, int NW, int D, typename QT, int KVF>
+__global__ void __launch_bounds__(NW * 64)
+sas_fwd_kernel(const FwdParams p) {
+  using C = Cfg<HW, NW, D, QT, KVF>;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int item = (int)(blockIdx.x % kXcds) * p.per_xcd + (int)(blockIdx.x / kXcds);
+  if (item >= p.items) return;
+  Tok k = item_of(p);
+  Fwd<HW, NW, D, QT, KVF> f(p, lane, wave);
+  const int hq = k.hg * (16 * HW) + f.hw * 16 + f.c16;
+  // Q^T operand in registers (head hq, channels ks*32 + 8g .. +8), loaded
+  // behind the block-table reads of the slot resolution
+  resolve<NW * 64>(p, k, tid, lane, wave, [&] {
+    const uint4* qp = reinterpret_cast<const uint4*>(p.q + ((size_t)k.t * p.H + hq) * D * 2);
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) f.qf[ks] = qp[ks * 4 + f.g];
+  });
+  const int nvalid = k.nvalid;
+
+  // key-group shares: whole steps, group 0 first
+  const int per = ((nvalid + C::KW * C::TR - 1) / (C::KW * C::TR)) * C::TR;
   const int gbeg = min(nvalid, f.kw * per);
-  f.rows = lds_rows + gbeg;
+  f.rbeg = gbeg;
+  f.ring = f.kw * C::NST * C::SLOT;
   f.nrows = min(nvalid, gbeg + per) - gbeg;
-  f.nsteps = (f.nrows + kTR - 1) / kTR;
-  f.nsteps_max = per / kTR;
+  f.nsteps = (f.nrows + C::TR - 1) / C::TR;
+  f.nsteps_max = per / C::TR;
   f.dummy = nvalid > 0 ? lds_rows[0] : 0;
 
   // retire every load the compiler tracks (Q, tables, indices) before the
@@ -585,163 +868,241 @@ sas_fwd_kernel(const FwdParams p) {
   f.m_run = seed_sink ? p.sinks[hq] * kLog2e : -INFINITY;
   f.l_run = seed_sink ? 1.f : 0.f;
 #pragma unroll
-  for (int i = 0; i < kDV / 16; ++i) f.acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < C::NTL; ++i) f.acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // ---- 2./3. pipelined step loop of this wave's key-group -----------------
-  if (f.kw == 0) f.template run_group<0>();
-  if constexpr (C::KW > 1) { if (f.kw == 1) f.template run_group<1>(); }
-  if constexpr (C::KW > 2) { if (f.kw == 2) f.template run_group<2>(); }
-  if constexpr (C::KW > 3) { if (f.kw == 3) f.template run_group<3>(); }
-
-  // ---- 4. merge key-groups, epilogue --------------------------------------
-  float M = f.m_run, L = f.l_run, w_self = 1.f;
-  if constexpr (C::KW > 1) {
-    if (f.g == 0) { lds_ml[wave][0][f.c16] = f.m_run; lds_ml[wave][1][f.c16] = f.l_run; }
-    __syncthreads();
-    M = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < C::KW; ++k) M = fmaxf(M, lds_ml[k * HW + f.hw][0][f.c16]);
-    L = 0.f;
-#pragma unroll
-    for (int k = 0; k < C::KW; ++k) {
-      const float mk = lds_ml[k * HW + f.hw][0][f.c16];
-      const float wk = mk == -INFINITY ? 0.f : exp2f(mk - M);
-      L += wk * lds_ml[k * HW + f.hw][1][f.c16];
-      if (k == f.kw) w_self = wk;
-    }
-    // scaled O of every wave -> its own slot as [head 16][512] fp32 (32 KB)
-    float* obuf = reinterpret_cast<float*>(slot_by_index(wave));
-#pragma unroll
-    for (int mt = 0; mt < kDV / 16; ++mt) {
-      const f32x4 v = f.acc[mt] * w_self;
-      *reinterpret_cast<float4*>(obuf + f.c16 * kDV + mt * 16 + f.g * 4) =
-          make_float4(v[0], v[1], v[2], v[3]);
-    }
-    __syncthreads();
-  }
-
-  const int nhead_wg = 16 * HW;
-  if constexpr (C::KW == 1) {
-    if (p.nsplit == 1) {
-      const float inv = padded ? 0.f : 1.f / L;
-      uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + ((size_t)t * p.H + hq) * kDV;
-#pragma unroll
-      for (int mt = 0; mt < kDV / 16; ++mt) {
-        const uint32_t w0 = to_bits<QT>(f.acc[mt][0] * inv) | (to_bits<QT>(f.acc[mt][1] * inv) << 16);
-        const uint32_t w1 = to_bits<QT>(f.acc[mt][2] * inv) | (to_bits<QT>(f.acc[mt][3] * inv) << 16);
-        *reinterpret_cast<uint2*>(op + mt * 16 + f.g * 4) = make_uint2(w0, w1);
-      }
-      if (f.g == 0) p.lse[(size_t)t * p.H + hq] = padded ? 0.f : M * kLn2 + logf(L);
-    } else {
-      const size_t row = ((size_t)t * p.nsplit + sp) * p.H + hq;
-      float* po = p.part_o + row * kDV;
-#pragma unroll
-      for (int mt = 0; mt < kDV / 16; ++mt)
-        *reinterpret_cast<float4*>(po + mt * 16 + f.g * 4) =
-            make_float4(f.acc[mt][0], f.acc[mt][1], f.acc[mt][2], f.acc[mt][3]);
-      if (f.g == 0) {
-        p.part_ml[row * 2 + 0] = M;
-        p.part_ml[row * 2 + 1] = padded ? -1.f : L;  // l < 0 marks a padded token
-      }
-    }
-  } else {
-    // every thread sums (head, 4 channels) items over the KW waves of its head-wave
-    const float* mlb = &lds_ml[0][0][0];
-    for (int e = tid; e < nhead_wg * (kDV / 4); e += 256) {
-      const int hh = e / (kDV / 4), c4 = e % (kDV / 4);
-      const int hwi = hh >> 4, hl = hh & 15;
-      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-      for (int k = 0; k < C::KW; ++k) {
-        const float* ob = reinterpret_cast<const float*>(slot_by_index(k * HW + hwi));
-        const float4 v = *reinterpret_cast<const float4*>(ob + hl * kDV + c4 * 4);
-        o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
-      }
-      const int h = hg * nhead_wg + hh;
-      if (p.nsplit == 1) {
-        // recompute this head's merged sum (the seed sink sits in key-group 0)
-        float Mh = -INFINITY, Lh = 0.f;
-#pragma unroll
-        for (int k = 0; k < C::KW; ++k) Mh = fmaxf(Mh, mlb[((k * HW + hwi) * 2 + 0) * 16 + hl]);
-#pragma unroll
-        for (int k = 0; k < C::KW; ++k) {
-          const float mk = mlb[((k * HW + hwi) * 2 + 0) * 16 + hl];
-          Lh += (mk == -INFINITY ? 0.f : exp2f(mk - Mh)) * mlb[((k * HW + hwi) * 2 + 1) * 16 + hl];
-        }
-        const float inv = padded ? 0.f : 1.f / Lh;
-        const uint32_t w0 = to_bits<QT>(o.x * inv) | (to_bits<QT>(o.y * inv) << 16);
-        const uint32_t w1 = to_bits<QT>(o.z * inv) | (to_bits<QT>(o.w * inv) << 16);
-        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + ((size_t)t * p.H + h) * kDV + c4 * 4) =
-            make_uint2(w0, w1);
-        if (c4 == 0) p.lse[(size_t)t * p.H + h] = padded ? 0.f : Mh * kLn2 + logf(Lh);
-      } else {
-        const size_t row = ((size_t)t * p.nsplit + sp) * p.H + h;
-        *reinterpret_cast<float4*>(p.part_o + row * kDV + c4 * 4) = o;
-        if (c4 == 0) {
-          float Mh = -INFINITY, Lh = 0.f;
-#pragma unroll
-          for (int k = 0; k < C::KW; ++k) Mh = fmaxf(Mh, mlb[((k * HW + hwi) * 2 + 0) * 16 + hl]);
-#pragma unroll
-          for (int k = 0; k < C::KW; ++k) {
-            const float mk = mlb[((k * HW + hwi) * 2 + 0) * 16 + hl];
-            Lh += (mk == -INFINITY ? 0.f : exp2f(mk - Mh)) * mlb[((k * HW + hwi) * 2 + 1) * 16 + hl];
-          }
-          p.part_ml[row * 2 + 0] = Mh;
-          p.part_ml[row * 2 + 1] = padded ? -1.f : Lh;
-        }
-      }
-    }
-  }
+  f.run();
+  epilogue<HW, NW, C::CS, QT>(p, k, tid, wave, lane, f.m_run, f.l_run, f.acc);
 }
 
 // ---------------------------------------------------------------------------
-// split-KV combine
+// decode kernel: every wave streams its own rows through registers (HW = 1)
+// ---------------------------------------------------------------------------
+//
+// A wave owns 16 heads and a contiguous share of the workgroup's rows, in
+// steps of 16 rows. Each lane loads its part of a step's rows straight into
+// the QK^T A-operand layout (row c16, channels 8(4ks+g) .. +8 for k-step
+// ks: one 16-byte load per k-step), NP steps ahead, so up to NP x 18 KB per
+// wave are in flight with no LDS staging; the QK^T MFMAs read those
+// registers. Only the V half (channels 0..511) passes through LDS, written
+// from the same registers into a per-wave tile that the PV operand reads
+// transposed. fp8 rows are dequantised in registers on the way.
+
+template <int D, typename QT, int KVF>
+struct Dec {
+  static constexpr int KS = D / 32;          // k-steps per row (chunks per lane)
+  static constexpr int NP = 3;               // steps in flight per wave
+  static constexpr int VCH = kDV / 8;        // chunks per V row
+  static constexpr int VT = 16 * VCH;        // chunks per V tile
+  static constexpr int ROWB = KVF ? kRow656 : D * 2;
+  static_assert(!KVF || D == 576, "fp8 rows carry 576 channels");
+  static_assert(4 * VT <= kLdsRows * kChunksMax, "V tiles fit");
+
+  struct Stage {
+    uint4 k[KVF ? 2 : KS];    // bf16 chunks (fp8: the two rope chunks)
+    uint2 l8[KVF ? 16 : 1];   // fp8: 8 latent bytes per k-step
+    float4 sc;                // fp8: the row's 4 scales
+  };
+
+  const FwdParams& p;
+  const int lane, c16, g;
+  int rbeg, nrows, nsteps, dummy, vt;
+  uint4 qf[KS];
+  float m_run, l_run;
+  f32x4 acc[kDV / 16];
+
+  __device__ Dec(const FwdParams& p_, int lane_) : p(p_), lane(lane_), c16(lane_ & 15), g(lane_ >> 4) {}
+
+  __device__ __forceinline__ const uint8_t* row_ptr(int id) const {
+    return id >= 0 ? p.ori_kv + (size_t)id * ROWB : p.cmp_kv + (size_t)(-id - 2) * ROWB;
+  }
+
+  // Step `step` of this wave into a stage. Loads are issued for every stage
+  // unconditionally, so the compiler's vmcnt bookkeeping sees the same load
+  // sequence on every path and waits exactly for the stage in use; a step
+  // past the end parks all lanes on one address (one cache line per load).
+  __device__ __forceinline__ void load(Stage& st, int step) const {
+    const int i = step * 16 + c16;
+    const bool live = step < nsteps;
+    const int id = lds_rows[rbeg + min(i, max(nrows - 1, 0))];
+    const uint8_t* src = row_ptr(live && i < nrows ? id : dummy);
+    const int gm = live ? g : 0, lm = live ? 1 : 0;
+    if constexpr (!KVF) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) st.k[ks] = *reinterpret_cast<const uint4*>(src + lm * (4 * ks + gm) * 16);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks) st.l8[ks] = *reinterpret_cast<const uint2*>(src + lm * (4 * ks + gm) * 8);
+      st.sc = *reinterpret_cast<const float4*>(src + lm * 512);
+      st.k[0] = *reinterpret_cast<const uint4*>(src + lm * (528 + gm * 16));
+      st.k[1] = *reinterpret_cast<const uint4*>(src + lm * (528 + (4 + gm) * 16));
+    }
+  }
+
+  // bf16 A-operand chunk 4ks + g of the lane's row
+  __device__ __forceinline__ uint4 kchunk(const Stage& st, int ks) const {
+    if constexpr (!KVF) {
+      return st.k[ks];
+    } else {
+      if (ks >= 16) return st.k[ks - 16];
+      const float sc = ks < 4 ? st.sc.x : ks < 8 ? st.sc.y : ks < 12 ? st.sc.z : st.sc.w;
+      const uint32_t w[2] = {st.l8[ks].x, st.l8[ks].y};
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t b0 = (w[i >> 1] >> ((i & 1) * 16)) & 0xffu;
+        const uint32_t b1 = (w[i >> 1] >> ((i & 1) * 16 + 8)) & 0xffu;
+        o[i] = f32_to_bf16_bits(e4m3_to_f32(b0) * sc) | (f32_to_bf16_bits(e4m3_to_f32(b1) * sc) << 16);
+      }
+      return make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+
+  template <int J, bool REFILL>
+  __device__ __forceinline__ void step(Stage (&st)[NP], int it0) {
+    const int it = it0 + J;
+    const int nk = min(16, nrows - it * 16);
+    uint4 kf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = kchunk(st[J], ks);
+    // V half -> this wave's LDS tile (row c16, chunk 4ks + g, swizzled)
+    const int vsw_w = swz(c16);
+#pragma unroll
+    for (int ks = 0; ks < VCH / 4; ++ks) lds_ring[vt + c16 * VCH + ((4 * ks + g) ^ vsw_w)] = kf[ks];
+    // S^T[16 keys x 16 heads] = K . Q^T, even / odd k-steps in two chains
+    f32x4 se = f32x4{0.f, 0.f, 0.f, 0.f}, so = se;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks & 1) so = mfma32k<QT>(kf[ks], qf[ks], so);
+      else se = mfma32k<QT>(kf[ks], qf[ks], se);
+    }
+    // the stage's registers are consumed: refill them NP steps ahead
+    if constexpr (REFILL) load(st[J], it + NP);
+    se += so;
+    float sv[4];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x = g * 4 + j < nk ? se[j] * p.scale_log2 : -INFINITY;
+      sv[j] = x;
+      mloc = fmaxf(mloc, x);
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    // lazy rescale (see Fwd::compute)
+    if (__ballot(mloc > m_run + kLazyLog2)) {
+      const float m_new = fmaxf(m_run, mloc);
+      const float alpha = exp2f(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int i = 0; i < kDV / 16; ++i) acc[i] *= alpha;
+    }
+    float pv[4], lsum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pv[j] = exp2f(sv[j] - m_run);
+      lsum += pv[j];
+    }
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    l_run += lsum;
+    const uint2 pfrag = make_uint2(to_bits<QT>(pv[0]) | (to_bits<QT>(pv[1]) << 16),
+                                   to_bits<QT>(pv[2]) | (to_bits<QT>(pv[3]) << 16));
+    // O^T[512 x 16] += V^T . P^T: one transposed read per 16-channel tile
+    // (rows 4g + c16/4, channels mt*16 + 4*(c16&3)), 16x16x16 MFMA
+    const int vr = 4 * g + (c16 >> 2);
+    const int vsw = swz(vr);
+    const int vb = (c16 & 3) >> 1;
+    const char* vbase = reinterpret_cast<const char*>(&lds_ring[vt + vr * VCH]) + (c16 & 1) * 8;
+    int voff[4];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) voff[q4] = ((2 * q4 + vb) ^ vsw) * 16;
+    auto vfrag = [&](int mt) {
+      const char* a0 = vbase + (mt >> 2) * 128 + voff[mt & 3];
+      return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a0)));
+    };
+    constexpr int kPf = 8;
+    uint2 vf[kPf];
+#pragma unroll
+    for (int i = 0; i < kPf; ++i) vf[i] = vfrag(i);
+#pragma unroll
+    for (int mt = 0; mt < kDV / 16; ++mt) {
+      const uint2 a = vf[mt % kPf];
+      if (mt + kPf < kDV / 16) vf[mt % kPf] = vfrag(mt + kPf);
+      acc[mt] = mfma16k<QT>(a, pfrag, acc[mt]);
+    }
+  }
+
+  // Whole groups of NP steps in the loop (every step refills its stage),
+  // the remaining 0..NP-1 steps after it (no refills).
+  __device__ __forceinline__ void run() {
+    Stage st[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) load(st[j], j);
+    int it0 = 0;
+    for (; it0 + NP <= nsteps; it0 += NP) {
+      step<0, true>(st, it0);
+      step<1, true>(st, it0);
+      step<2, true>(st, it0);
+    }
+    const int r = nsteps - it0;
+    if (r > 0) step<0, false>(st, it0);
+    if (r > 1) step<1, false>(st, it0);
+  }
+};
+
+template <int D, typename QT, int KVF>
+__global__ void __launch_bounds__(256)
+sas_dec_kernel(const FwdParams p) {
+  using C = Dec<D, QT, KVF>;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int item = (int)(blockIdx.x % kXcds) * p.per_xcd + (int)(blockIdx.x / kXcds);
+  if (item >= p.items) return;
+  Tok k = item_of(p);
+  C f(p, lane);
+  resolve<256>(p, k, tid, lane, wave, [] {});
+  const int nvalid = k.nvalid;
+  const int hq = k.hg * 16 + f.c16;
+  // key-group share of wave `wave`: whole 16-row steps, wave 0 first
+  const int per = ((nvalid + 63) >> 6) << 4;
+  const int gbeg = min(nvalid, wave * per);
+  f.rbeg = gbeg;
+  f.nrows = min(nvalid, gbeg + per) - gbeg;
+  f.nsteps = (f.nrows + 15) >> 4;
+  f.dummy = nvalid > 0 ? lds_rows[0] : 0;
+  f.vt = wave * C::VT;
+  // Q^T operand in registers (head hq, channels ks*32 + 8g .. +8), ahead of
+  // the first K loads
+  {
+    const uint4* qp = reinterpret_cast<const uint4*>(p.q + ((size_t)k.t * p.H + hq) * D * 2);
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) f.qf[ks] = qp[ks * 4 + f.g];
+  }
+  const bool seed_sink = p.nsplit == 1 && wave == 0;
+  f.m_run = seed_sink ? p.sinks[hq] * kLog2e : -INFINITY;
+  f.l_run = seed_sink ? 1.f : 0.f;
+#pragma unroll
+  for (int i = 0; i < kDV / 16; ++i) f.acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (f.nsteps > 0) f.run();
+  epilogue<1, 4, 1, QT>(p, k, tid, wave, lane, f.m_run, f.l_run, f.acc);
+}
+
+// ---------------------------------------------------------------------------
+// split-KV combine (separate launch; used with SAS_FWD_NO_COMBINE)
 // ---------------------------------------------------------------------------
 
 constexpr int kCombineThreads = 256;
 constexpr int kMaxCombineSplits = 64;
 
-// One workgroup per (token, 2 heads), thread = (head, 4 channels). Each
-// thread derives its head's merge weights from the small (m, l) partials and
-// streams its S partial rows once; loads are independent, so they overlap.
+// One workgroup per (token, 2 heads), thread = (head, 4 channels).
 template <typename QT>
 __global__ void __launch_bounds__(kCombineThreads)
-sas_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
-                   const float* __restrict__ sinks, uint8_t* __restrict__ out,
-                   float* __restrict__ lse, int S, int H) {
+sas_combine_kernel(const FwdParams p) {
   constexpr int kHeads = kCombineThreads / (kDV / 4);  // 2
-  const int nhb = (H + kHeads - 1) / kHeads;
+  const int nhb = (p.H + kHeads - 1) / kHeads;
   const int t = blockIdx.x / nhb;
-  const int c4 = threadIdx.x % (kDV / 4);
-  const int h = (blockIdx.x % nhb) * kHeads + threadIdx.x / (kDV / 4);
-  if (h >= H) return;
-  const size_t row0 = (size_t)t * S * H + h;
-  const float sink2 = sinks[h] * kLog2e;
-  float M = sink2;
-  bool pad = false;
-#pragma unroll 8
-  for (int s = 0; s < S; ++s) {
-    const float2 ml = *reinterpret_cast<const float2*>(part_ml + (row0 + (size_t)s * H) * 2);
-    M = fmaxf(M, ml.x);
-    pad |= ml.y < 0.f;
-  }
-  float L = exp2f(sink2 - M);
-  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-  for (int s = 0; s < S; ++s) {
-    const size_t r = row0 + (size_t)s * H;
-    const float2 ml = *reinterpret_cast<const float2*>(part_ml + r * 2);
-    const float4 v = *reinterpret_cast<const float4*>(part_o + r * kDV + c4 * 4);
-    const float w = exp2f(ml.x - M);
-    L += w * ml.y;
-    o.x += w * v.x; o.y += w * v.y; o.z += w * v.z; o.w += w * v.w;
-  }
-  const float il = pad ? 0.f : 1.f / L;
-  const uint32_t w0 = to_bits<QT>(o.x * il) | (to_bits<QT>(o.y * il) << 16);
-  const uint32_t w1 = to_bits<QT>(o.z * il) | (to_bits<QT>(o.w * il) << 16);
-  *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + ((size_t)t * H + h) * kDV + c4 * 4) =
-      make_uint2(w0, w1);
-  if (c4 == 0) lse[(size_t)t * H + h] = pad ? 0.f : M * kLn2 + logf(L);
+  const int h0 = (blockIdx.x % nhb) * kHeads;
+  merge_partials<QT>(p, t, h0, min(kHeads, p.H - h0), threadIdx.x, kCombineThreads);
 }
 
 // ---------------------------------------------------------------------------
@@ -749,7 +1110,7 @@ sas_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ p
 // ---------------------------------------------------------------------------
 
 struct Plan {
-  int hw, nhg, nslots, nsplit, sps;
+  int hw, nw, nhg, nslots, nsplit, sps;
   size_t ws;
 };
 
@@ -763,30 +1124,41 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   if (a->flags & ~SAS_FWD_NO_COMBINE) return sas::set_error(SAS_EINVAL, "unknown flags 0x%x", a->flags);
   if (a->win_left < 0 || a->win_left > 8191) return sas::set_error(SAS_EINVAL, "win_left out of range");
   if (a->scenario >= SAS_CFA && (a->cmp_ratio < 1 || a->K < 0)) return sas::set_error(SAS_EINVAL, "bad cmp_ratio/K");
-  const bool fp8 = a->kv_dtype == SAS_DT_FP8_E4M3_ROW656;
-  // head-waves per workgroup: 4 whenever H allows it (64 heads share every
-  // gathered tile, so each KV row crosses HBM->LDS once per token); 2 or 1
-  // only for head counts that are not a multiple of 64.
+  pl->nslots = a->win_left + 1 + (a->scenario >= SAS_CFA ? (int)a->K : 0);
+  const long long T = std::max<long long>(a->T, 1);
   int hw = a->head_waves;
-  if (hw <= 0) hw = 4;
+  int ns = a->num_splits;
+  if (hw <= 0) {
+    // Heads sharing one gathered tile inside a workgroup (16 per wave). With
+    // many tokens every workgroup holds 64 heads: each row crosses L2 -> CU
+    // once per token. With few tokens, 32-head groups (2 head-waves x 2
+    // key-groups) spread a token over twice the workgroups for the same split
+    // count: half the fp32 split partials of 64-head groups at the same grid
+    // size, for each row read twice through L2 (measured best for the
+    // 32-token, 64-head decode).
+    if (a->H % 64 == 0 && T * (a->H / 64) >= 2 * kCus) hw = 4;
+    else if (a->H % 32 == 0) hw = 2;
+    else hw = 1;
+  }
   if (hw != 1 && hw != 2 && hw != 4) return sas::set_error(SAS_EINVAL, "head_waves must be 1, 2 or 4");
   while (hw > 1 && a->H % (16 * hw)) hw >>= 1;
-  if (fp8) {  // fp8 staging registers only fit with 4 head-waves (or 2 when H = 32k)
-    if (a->H % 32) return sas::set_error(SAS_EINVAL, "fp8 cache rows need H a multiple of 32");
-    hw = a->H % 64 ? 2 : 4;
-  }
+  int nw = a->waves;
+  // 8 waves (two per SIMD, each holding half of its heads' O channels) are
+  // available on request; the fp8 staging registers only fit 4 waves
+  if (nw == 8 && a->kv_dtype == SAS_DT_FP8_E4M3_ROW656) nw = 4;
+  if (nw <= 0) nw = 4;
+  if (nw != 4 && nw != 8) return sas::set_error(SAS_EINVAL, "waves must be 4 or 8");
+  if (hw == 1) nw = 4;
+  pl->nw = nw;
   pl->hw = hw;
   pl->nhg = (int)a->H / (16 * hw);
-  pl->nslots = a->win_left + 1 + (a->scenario >= SAS_CFA ? (int)a->K : 0);
-  int ns = a->num_splits;
   if (ns <= 0) {
-    // about half a workgroup per CU: every extra split adds a partial
-    // write + combine read of 2 KB per head, which past ~128 workgroups
-    // costs more than the extra streaming parallelism gains; splits no
-    // smaller than one 32-row step
-    const long long items = std::max<long long>(1, (long long)a->T * pl->nhg);
-    const long long want = (kSplitTarget + items - 1) / items;
-    const int max_by_step = std::max(1, (pl->nslots + kTR - 1) / kTR);
+    // one workgroup per CU: split the slots until the grid covers the chip,
+    // keeping every split long enough for one step of each key-group
+    const long long items = T * pl->nhg;
+    const long long want = (kCus + items - 1) / items;
+    const int min_sps = hw == 1 ? 64 : hw == 2 ? 64 : 32;
+    const int max_by_step = std::max(1, (pl->nslots + min_sps - 1) / min_sps);
     ns = (int)std::min<long long>(std::max<long long>(want, 1), max_by_step);
   }
   ns = std::max(1, std::min(ns, kMaxCombineSplits));
@@ -803,22 +1175,44 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   return SAS_OK;
 }
 
-template <int HW, int D, typename QT, int KVF>
+template <int HW, int NW, int D, typename QT, int KVF>
 int launch_fwd(const FwdParams& fp, int nblocks, hipStream_t st) {
-  hipLaunchKernelGGL((sas_fwd_kernel<HW, D, QT, KVF>), dim3(nblocks), dim3(256), 0, st, fp);
+  hipLaunchKernelGGL((sas_fwd_kernel<HW, NW, D, QT, KVF>), dim3(nblocks), dim3(NW * 64), 0, st, fp);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return sas::set_error(SAS_ELAUNCH, "sas_fwd launch: %s", hipGetErrorString(e));
   return SAS_OK;
 }
 
 template <int D, typename QT, int KVF>
-int dispatch_hw(int hw, const FwdParams& fp, int nb, hipStream_t st) {
-  if constexpr (!KVF) {
-    if (hw == 1) return launch_fwd<1, D, QT, KVF>(fp, nb, st);
-  }
-  if (hw == 2) return launch_fwd<2, D, QT, KVF>(fp, nb, st);
-  if (hw == 4) return launch_fwd<4, D, QT, KVF>(fp, nb, st);
+int launch_dec(const FwdParams& fp, int nblocks, hipStream_t st) {
+  hipLaunchKernelGGL((sas_dec_kernel<D, QT, KVF>), dim3(nblocks), dim3(256), 0, st, fp);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return sas::set_error(SAS_ELAUNCH, "sas_dec launch: %s", hipGetErrorString(e));
+  return SAS_OK;
+}
+
+template <int D, typename QT, int KVF>
+int dispatch_hw(int hw, int nw, const FwdParams& fp, int nb, hipStream_t st) {
+  if (hw == 1) return launch_dec<D, QT, KVF>(fp, nb, st);
+  if (hw == 2 && nw == 4) return launch_fwd<2, 4, D, QT, KVF>(fp, nb, st);
+  if (hw == 2 && nw == 8) return launch_fwd<2, 8, D, QT, KVF>(fp, nb, st);
+  if (hw == 4 && nw == 4) return launch_fwd<4, 4, D, QT, KVF>(fp, nb, st);
+  if (hw == 4 && nw == 8) return launch_fwd<4, 8, D, QT, KVF>(fp, nb, st);
   return sas::set_error(SAS_EINVAL, "unsupported head grouping");
+}
+
+int launch_combine(const FwdParams& fp, int out_dtype, hipStream_t st) {
+  constexpr int kHeads = kCombineThreads / (kDV / 4);
+  const dim3 grid((unsigned)(fp.T * ((fp.H + kHeads - 1) / kHeads)));
+  if (out_dtype == SAS_DT_BF16)
+    hipLaunchKernelGGL(sas_combine_kernel<__bf16>, grid, dim3(kCombineThreads), 0, st, fp);
+  else if (out_dtype == SAS_DT_FP16)
+    hipLaunchKernelGGL(sas_combine_kernel<_Float16>, grid, dim3(kCombineThreads), 0, st, fp);
+  else
+    return sas::set_error(SAS_EINVAL, "combine: bad out dtype");
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return sas::set_error(SAS_ELAUNCH, "sas_combine launch: %s", hipGetErrorString(e));
+  return SAS_OK;
 }
 
 int combine_impl(const SasCombineArgs* a, hipStream_t st) {
@@ -827,19 +1221,14 @@ int combine_impl(const SasCombineArgs* a, hipStream_t st) {
   if (a->DV != kDV || a->S < 1 || a->S > kMaxCombineSplits || a->H < 1 || a->T < 0)
     return sas::set_error(SAS_EINVAL, "combine: bad dims (S must be 1..64, DV 512)");
   if (a->T == 0) return SAS_OK;
-  constexpr int kHeads = kCombineThreads / (kDV / 4);
-  const dim3 grid((unsigned)(a->T * ((a->H + kHeads - 1) / kHeads)));
-  if (a->out_dtype == SAS_DT_BF16)
-    hipLaunchKernelGGL(sas_combine_kernel<__bf16>, grid, dim3(kCombineThreads), 0, st, a->part_o,
-                       a->part_ml, a->sinks, (uint8_t*)a->out, a->lse, (int)a->S, (int)a->H);
-  else if (a->out_dtype == SAS_DT_FP16)
-    hipLaunchKernelGGL(sas_combine_kernel<_Float16>, grid, dim3(kCombineThreads), 0, st, a->part_o,
-                       a->part_ml, a->sinks, (uint8_t*)a->out, a->lse, (int)a->S, (int)a->H);
-  else
-    return sas::set_error(SAS_EINVAL, "combine: bad out dtype");
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return sas::set_error(SAS_ELAUNCH, "sas_combine launch: %s", hipGetErrorString(e));
-  return SAS_OK;
+  FwdParams fp{};
+  fp.part_o = const_cast<float*>(a->part_o);
+  fp.part_ml = const_cast<float*>(a->part_ml);
+  fp.sinks = a->sinks;
+  fp.out = (uint8_t*)a->out;
+  fp.lse = a->lse;
+  fp.T = (int)a->T; fp.H = (int)a->H; fp.nsplit = (int)a->S;
+  return launch_combine(fp, a->out_dtype, st);
 }
 
 }  // namespace
@@ -881,7 +1270,7 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   if (pl.nsplit > 1 && (!a->workspace || a->workspace_bytes < pl.ws))
     return sas::set_error(SAS_ENOWS, "workspace of %zu bytes required", pl.ws);
 
-  FwdParams fp;
+  FwdParams fp{};
   fp.q = (const uint8_t*)a->q;
   fp.ori_kv = (const uint8_t*)a->ori_kv;
   fp.ori_bt = a->ori_block_table;
@@ -894,8 +1283,10 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   fp.sinks = a->sinks;
   fp.out = (uint8_t*)a->out;
   fp.lse = a->lse;
-  fp.part_o = pl.nsplit > 1 ? (float*)a->workspace : nullptr;
-  fp.part_ml = pl.nsplit > 1 ? (float*)a->workspace + (size_t)a->T * pl.nsplit * a->H * kDV : nullptr;
+  if (pl.nsplit > 1) {
+    fp.part_o = (float*)a->workspace;
+    fp.part_ml = (float*)a->workspace + (size_t)a->T * pl.nsplit * a->H * kDV;
+  }
   fp.T = (int)a->T; fp.B = (int)a->B; fp.H = (int)a->H;
   fp.ori_bs = (int)a->ori_block_size; fp.ori_bt_stride = (int)a->ori_bt_stride;
   fp.ori_nblocks = (int)a->ori_num_blocks;
@@ -911,23 +1302,15 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   const int nblocks = fp.per_xcd * kXcds;
   hipStream_t st = (hipStream_t)stream;
 
-  if (fp8) rc = dispatch_hw<576, __bf16, 1>(pl.hw, fp, nblocks, st);
+  if (fp8) rc = dispatch_hw<576, __bf16, 1>(pl.hw, pl.nw, fp, nblocks, st);
   else if (a->q_dtype == SAS_DT_BF16)
-    rc = a->D == 576 ? dispatch_hw<576, __bf16, 0>(pl.hw, fp, nblocks, st)
-                     : dispatch_hw<512, __bf16, 0>(pl.hw, fp, nblocks, st);
+    rc = a->D == 576 ? dispatch_hw<576, __bf16, 0>(pl.hw, pl.nw, fp, nblocks, st)
+                     : dispatch_hw<512, __bf16, 0>(pl.hw, pl.nw, fp, nblocks, st);
   else
-    rc = a->D == 576 ? dispatch_hw<576, _Float16, 0>(pl.hw, fp, nblocks, st)
-                     : dispatch_hw<512, _Float16, 0>(pl.hw, fp, nblocks, st);
-  if (rc) return rc;
-  if (pl.nsplit > 1 && !(a->flags & SAS_FWD_NO_COMBINE)) {
-    SasCombineArgs ca;
-    ca.part_o = fp.part_o; ca.part_ml = fp.part_ml; ca.sinks = a->sinks;
-    ca.out = a->out; ca.lse = a->lse;
-    ca.T = a->T; ca.S = pl.nsplit; ca.H = a->H; ca.DV = kDV;
-    ca.out_dtype = a->q_dtype;
-    return combine_impl(&ca, st);
-  }
-  return SAS_OK;
+    rc = a->D == 576 ? dispatch_hw<576, _Float16, 0>(pl.hw, pl.nw, fp, nblocks, st)
+                     : dispatch_hw<512, _Float16, 0>(pl.hw, pl.nw, fp, nblocks, st);
+  if (rc || pl.nsplit == 1 || (a->flags & SAS_FWD_NO_COMBINE)) return rc;
+  return launch_combine(fp, a->q_dtype, st);
 }
 
 extern "C" int sas_combine_v1(const SasCombineArgs* a, void* stream) {

@@ -113,9 +113,11 @@ typedef struct SasFwdArgs {
   float softmax_scale;
   int32_t num_splits;            /* KV splits per token; 0 = choose automatically */
   int32_t head_waves;            /* waves sharing each KV tile (16 heads each): 1, 2, 4;
-                                    the other 4/head_waves groups stream disjoint rows;
+                                    the other waves/head_waves groups stream disjoint rows;
                                     0 = choose automatically */
   int32_t flags;                 /* SAS_FWD_* bits, 0 by default */
+  int32_t waves;                 /* waves per workgroup: 4 or 8 (head_waves 1: 4);
+                                    0 = choose automatically */
 } SasFwdArgs;
 
 /* SasFwdArgs.flags: with more than one split, stop after the split kernel and
