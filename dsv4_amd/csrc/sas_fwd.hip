@@ -33,178 +33,10 @@
 // decode), :628-722 (window / compressed masks), :594-617 (sink seed),
 // :877 (P cast), :1135-1145 (LSE), and golden.py:69-204.
 
-#include <hip/hip_runtime.h>
+#include "sas_kern.h"
 
-#include <algorithm>
-#include <climits>
-#include <cmath>
-#include <cstdint>
-
-#include "../../include/sas.h"
-#include "sas_common.h"
-
-#define LDS_AS __attribute__((address_space(3)))
-
+namespace sas {
 namespace {
-
-constexpr int kDV = 512;          // output / V channels
-constexpr int kMaxSlots = 1280;   // slot range one workgroup may own
-constexpr int kRoundsMax = kMaxSlots / 256;  // slot rounds at 256 threads
-constexpr int kMaxWaves = 8;
-constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dealt round-robin
-constexpr int kCus = 256;         // MI355X compute units (one forward workgroup each)
-constexpr int kRow656 = 656;      // fp8 cache row bytes
-constexpr int kChunksMax = 72;    // 16-byte chunks of a 576-channel bf16 row
-constexpr int kLdsRows = 128;     // rows of ring storage per workgroup
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-constexpr float kLazyLog2 = 8.f;   // O / l rescale threshold (log2 units)
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-
-__shared__ __attribute__((aligned(16))) uint4 lds_ring[kLdsRows * kChunksMax];  // 147,456 B
-__shared__ int lds_rows[kMaxSlots];
-__shared__ int lds_cnt[kRoundsMax][kMaxWaves];
-__shared__ float lds_ml[kMaxWaves][2][16];
-
-struct FwdParams {
-  const uint8_t* q;
-  const uint8_t* ori_kv;
-  const int32_t* ori_bt;
-  const uint8_t* cmp_kv;
-  const int32_t* cmp_bt;
-  const int32_t* cmp_idx;
-  const int32_t* q_prefix;
-  const int32_t* act_q;
-  const int32_t* act_kv;
-  const float* sinks;
-  uint8_t* out;
-  float* lse;
-  float* part_o;
-  float* part_ml;
-  int T, B, H;
-  int ori_bs, ori_bt_stride, ori_nblocks;
-  int cmp_bs, cmp_bt_stride, cmp_nblocks;
-  int K, scenario, cmp_ratio, win_left;
-  float scale_log2;
-  int nsplit, slots_per_split, nhg, items, per_xcd;
-};
-
-// ---------------------------------------------------------------------------
-// element helpers
-// ---------------------------------------------------------------------------
-
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite inputs)
-  return u >> 16;
-}
-
-__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
-  _Float16 h = (_Float16)f;
-  return (uint32_t)__builtin_bit_cast(uint16_t, h);
-}
-
-template <typename QT>
-__device__ __forceinline__ uint32_t to_bits(float f);
-template <>
-__device__ __forceinline__ uint32_t to_bits<__bf16>(float f) { return f32_to_bf16_bits(f); }
-template <>
-__device__ __forceinline__ uint32_t to_bits<_Float16>(float f) { return f32_to_f16_bits(f); }
-
-// OCP e4m3fn byte -> float (bias 7, subnormals m * 2^-9; 0x7f/0xff NaN are
-// never produced by the cache writer, which saturates at 448).
-__device__ __forceinline__ float e4m3_to_f32(uint32_t v) {
-  const uint32_t e = (v >> 3) & 0xfu, m = v & 7u;
-  float f = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * 0.001953125f;
-  return (v & 0x80u) ? -f : f;
-}
-
-// 16x16x32: A = 8 values of row l%16 (k = 8*(l/16)..), B likewise by column
-template <typename QT>
-__device__ __forceinline__ f32x4 mfma32k(const uint4& a, const uint4& b, const f32x4& c);
-template <>
-__device__ __forceinline__ f32x4 mfma32k<__bf16>(const uint4& a, const uint4& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-template <>
-__device__ __forceinline__ f32x4 mfma32k<_Float16>(const uint4& a, const uint4& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-// 16x16x16: A = 4 values of row l%16 (k = 4*(l/16)..), B likewise by column
-template <typename QT>
-__device__ __forceinline__ f32x4 mfma16k(const uint2& a, const uint2& b, const f32x4& c);
-template <>
-__device__ __forceinline__ f32x4 mfma16k<__bf16>(const uint2& a, const uint2& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
-                                                   __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
-}
-template <>
-__device__ __forceinline__ f32x4 mfma16k<_Float16>(const uint2& a, const uint2& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
-                                               __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
-}
-
-// Chunk swizzle inside each aligned group of 8 chunks of a row: row r keeps
-// logical chunk c at position c ^ swz(r). With it, 8 lanes reading the same
-// chunk of rows r..r+7 (QK^T operand) and 16 lanes reading 4 rows x 2 chunks
-// (transposed PV operand) each touch distinct banks.
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
-
-// 16 bytes per lane global -> LDS (lane i lands at lds_addr + 16 i). Issued
-// as inline asm so the compiler does not track it: its LDS-DMA tracking
-// cannot tell the slots apart for transposed LDS reads and would wait for
-// every load in flight. Completion is ordered explicitly with wait_vm<>()
-// (loads return in order, so the compiler's own vmcnt waits for its loads
-// stay conservative).
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
-  asm volatile(
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
-      :
-      : "v"(src), "s"(lds_addr)
-      : "memory", "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
-  return (uint32_t)(uintptr_t)(const LDS_AS void*)p;
-}
-
-// s_waitcnt vmcnt(N) leaving expcnt / lgkmcnt alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 63] known only at run time
-__device__ __forceinline__ void wait_vm_rt(int n) {
-  switch (n) {
-#define SAS_WAITCASE(k) case k: wait_vm<k>(); break;
-#define SAS_WAITCASE8(k) SAS_WAITCASE(k) SAS_WAITCASE(k + 1) SAS_WAITCASE(k + 2) SAS_WAITCASE(k + 3) \
-    SAS_WAITCASE(k + 4) SAS_WAITCASE(k + 5) SAS_WAITCASE(k + 6) SAS_WAITCASE(k + 7)
-    SAS_WAITCASE8(0) SAS_WAITCASE8(8) SAS_WAITCASE8(16) SAS_WAITCASE8(24)
-    SAS_WAITCASE8(32) SAS_WAITCASE8(40) SAS_WAITCASE8(48) SAS_WAITCASE8(56)
-#undef SAS_WAITCASE8
-#undef SAS_WAITCASE
-    default: wait_vm<0>(); break;
-  }
-}
-__device__ __forceinline__ void wait_lgkm0() {
-  __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
-}
-// LDS reads done, then a workgroup barrier (no memory fence: in-flight LDS
-// DMA of other slots keeps streaming across it).
-__device__ __forceinline__ void lds_barrier() {
-  wait_lgkm0();
-  __builtin_amdgcn_s_barrier();
-}
 
 // ---------------------------------------------------------------------------
 // forward kernel
@@ -545,208 +377,6 @@ struct Fwd {
     }
   }
 };
-
-template <typename QT>
-__device__ __forceinline__ void store_out4(const FwdParams& p, int t, int h, int c4, float4 o, float inv) {
-  const uint32_t w0 = to_bits<QT>(o.x * inv) | (to_bits<QT>(o.y * inv) << 16);
-  const uint32_t w1 = to_bits<QT>(o.z * inv) | (to_bits<QT>(o.w * inv) << 16);
-  *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + ((size_t)t * p.H + h) * kDV + c4 * 4) =
-      make_uint2(w0, w1);
-}
-
-// Merge the nsplit fp32 partials of (token t, heads [h0, h0 + nh)) with the
-// sink into out / lse: M = max(sink, m_i), L = 2^(sink-M) + sum_i l_i
-// 2^(m_i-M), out = sum_i 2^(m_i-M) O_i / L, lse = (M ln 2) + ln L (a running
-// merge over i, kB splits' loads in flight together). A negative l marks a
-// padded token (out = 0, lse = 0).
-template <typename QT>
-__device__ __forceinline__ void merge_partials(const FwdParams& p, int t, int h0, int nh, int tid,
-                                               int nthreads) {
-  constexpr int kB = 4;
-  const int S = p.nsplit;
-  const float* po = p.part_o + (size_t)t * S * p.H * kDV;
-  const float* pm = p.part_ml + (size_t)t * S * p.H * 2;
-  for (int e = tid; e < nh * (kDV / 4); e += nthreads) {
-    const int h = h0 + e / (kDV / 4), c4 = e % (kDV / 4);
-    float M = p.sinks[h] * kLog2e, L = 1.f;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    bool pad = false;
-    for (int s0 = 0; s0 < S; s0 += kB) {
-      float2 ml[kB];
-      float4 v[kB];
-#pragma unroll
-      for (int j = 0; j < kB; ++j) {
-        const size_t row = (size_t)min(s0 + j, S - 1) * p.H + h;
-        ml[j] = *reinterpret_cast<const float2*>(pm + row * 2);
-        v[j] = *reinterpret_cast<const float4*>(po + row * kDV + c4 * 4);
-      }
-#pragma unroll
-      for (int j = 0; j < kB; ++j) {
-        if (s0 + j >= S) break;
-        pad |= ml[j].y < 0.f;
-        if (ml[j].x > M) {
-          const float a = exp2f(M - ml[j].x);
-          L *= a; o.x *= a; o.y *= a; o.z *= a; o.w *= a;
-          M = ml[j].x;
-        }
-        const float w = ml[j].x == -INFINITY ? 0.f : exp2f(ml[j].x - M);
-        L += w * ml[j].y;
-        o.x += w * v[j].x; o.y += w * v[j].y; o.z += w * v[j].z; o.w += w * v[j].w;
-      }
-    }
-    store_out4<QT>(p, t, h, c4, o, pad ? 0.f : 1.f / L);
-    if (c4 == 0) p.lse[(size_t)t * p.H + h] = pad ? 0.f : M * kLn2 + logf(L);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// shared prologue: slot resolution
-// ---------------------------------------------------------------------------
-
-struct Tok {
-  int t, hg, sp;     // token, head group, KV split
-  int b, nvalid;     // batch, compacted rows in lds_rows
-  bool padded;       // (b, position) outside the batch's query length
-};
-
-__device__ __forceinline__ Tok item_of(const FwdParams& p) {
-  // XCD-aware item mapping: XCD x = blockIdx % 8 owns a contiguous item range,
-  // so all splits / head groups of a token (and neighbouring tokens) share L2.
-  const int item = (int)(blockIdx.x % kXcds) * p.per_xcd + (int)(blockIdx.x / kXcds);
-  Tok k;
-  const int per_tok = p.nhg * p.nsplit;
-  k.t = item / per_tok;
-  k.hg = (item % per_tok) / p.nsplit;
-  k.sp = item % p.nsplit;
-  k.b = 0; k.nvalid = 0; k.padded = true;
-  return k;
-}
-
-// Resolve the item's slot range to cache rows and compact the valid ones, in
-// slot order, into lds_rows[0, nvalid). Raw rows are stored as id >= 0,
-// compressed rows as -(id + 2). `mid` runs after the block-table loads are
-// issued (a caller can put its own loads behind them there).
-template <int NT, typename Mid>
-__device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int lane, int wave, Mid&& mid) {
-  constexpr int NWV = NT / 64;
-  constexpr int kRounds = (kMaxSlots + NT - 1) / NT;
-  static_assert(kRounds <= kRoundsMax && NWV <= kMaxWaves, "resolve geometry");
-  const int t = k.t;
-  const int wincap = p.win_left + 1;
-  const int nslots = wincap + (p.scenario >= SAS_CFA ? p.K : 0);
-  const int s0 = k.sp * p.slots_per_split;
-  const int s1 = min(s0 + p.slots_per_split, nslots);
-  const int nr = (s1 - s0 + NT - 1) / NT;   // slot rounds of NT (<= kRounds)
-
-  // ---- round trip 1: top-k indices and batch scalars ------------------------
-  int idxv[kRounds];
-#pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    idxv[r] = -1;
-    const int j = s0 + r * NT + tid;
-    if (r < nr && p.scenario == SAS_SCFA && j < s1 && j >= wincap)
-      idxv[r] = p.cmp_idx[(size_t)t * p.K + (j - wincap)];
-  }
-  int qp0 = INT_MAX, aq0 = 0, akv0 = 0;
-  if (lane < p.B) { qp0 = p.q_prefix[lane]; aq0 = p.act_q[lane]; akv0 = p.act_kv[lane]; }
-  // token -> (batch, position): largest b with q_prefix[b] <= t (q_prefix is
-  // non-decreasing), one ballot per 64 batches
-  int b = 0, aq = 0, akv = 0, qpb = 0;
-  {
-    uint64_t m = __ballot(qp0 <= t);
-    int n = __popcll(m);
-    if (n) { b = n - 1; qpb = __shfl(qp0, n - 1); aq = __shfl(aq0, n - 1); akv = __shfl(akv0, n - 1); }
-    for (int c = 64; n == 64 && c < p.B; c += 64) {
-      const int i = c + lane;
-      int qpi = INT_MAX, aqi = 0, akvi = 0;
-      if (i < p.B) { qpi = p.q_prefix[i]; aqi = p.act_q[i]; akvi = p.act_kv[i]; }
-      m = __ballot(qpi <= t);
-      n = __popcll(m);
-      if (n) { b = c + n - 1; qpb = __shfl(qpi, n - 1); aq = __shfl(aqi, n - 1); akv = __shfl(akvi, n - 1); }
-    }
-  }
-  const int spos = t - qpb;
-  const bool padded = spos < 0 || spos >= aq;
-  const int sg = akv - aq + spos;                              // causal position
-  const int nwin = (padded || sg < 0) ? 0 : min(sg, p.win_left) + 1;
-  const int wlo = sg - nwin + 1;                               // = max(sg - win_left, 0)
-  const int thr = (padded || sg + 1 <= 0) ? 0 : (sg + 1) / p.cmp_ratio;
-
-  // ---- round trip 2: block tables -------------------------------------------
-  // Every table read is issued unconditionally at a clamped, in-range
-  // address (validity is kept apart), so the reads of all rounds are in
-  // flight together and retire with one wait.
-  int rid[kRounds];
-  {
-    const int32_t* obt = p.ori_bt + (size_t)b * p.ori_bt_stride;
-    const int32_t* cbt = p.cmp_bt ? p.cmp_bt + (size_t)b * p.cmp_bt_stride : obt;
-    int phys[kRounds], off[kRounds];
-    bool ok[kRounds], ori[kRounds];
-#pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-      phys[r] = -1; ok[r] = false; ori[r] = true; off[r] = 0;
-      if (r >= nr) continue;   // uniform
-      const int j = s0 + r * NT + tid;
-      const bool live = j < s1 && !padded;
-      int blk;
-      if (j < wincap) {
-        const int pos = wlo + j;
-        blk = pos / p.ori_bs;
-        off[r] = pos - blk * p.ori_bs;
-        ok[r] = live && j < nwin && blk < p.ori_bt_stride;
-      } else {
-        const int idx = p.scenario == SAS_SCFA ? idxv[r] : j - wincap;
-        const int ic = max(idx, 0);
-        blk = ic / p.cmp_bs;
-        off[r] = ic - blk * p.cmp_bs;
-        ori[r] = false;
-        ok[r] = live && idx >= 0 && idx < thr && blk < p.cmp_bt_stride;
-      }
-      phys[r] = (ori[r] ? obt : cbt)[ok[r] ? blk : 0];
-    }
-    // the caller's loads go behind the table reads, so waiting for the
-    // tables leaves them in flight
-    asm volatile("" ::: "memory");
-    mid();
-    asm volatile("" ::: "memory");
-#pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-      rid[r] = -1;
-      if (ori[r]) {
-        if (ok[r] && phys[r] >= 0 && phys[r] < p.ori_nblocks) rid[r] = phys[r] * p.ori_bs + off[r];
-      } else {
-        if (ok[r] && phys[r] >= 0 && phys[r] < p.cmp_nblocks) rid[r] = -(phys[r] * p.cmp_bs + off[r] + 2);
-      }
-    }
-  }
-  // ---- compaction (ballot + per-wave counts) -------------------------------
-  uint64_t vmask[kRounds];
-#pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    vmask[r] = __ballot(rid[r] != -1);
-    if (r < nr && lane == 0) lds_cnt[r][wave] = __popcll(vmask[r]);
-  }
-  __syncthreads();
-  int nvalid = 0;
-#pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    if (r >= nr) break;
-    int wpre = 0, tot = 0;
-#pragma unroll
-    for (int w = 0; w < NWV; ++w) {
-      const int cw = lds_cnt[r][w];
-      wpre += w < wave ? cw : 0;
-      tot += cw;
-    }
-    if (rid[r] != -1)
-      lds_rows[nvalid + wpre + __popcll(vmask[r] & ((1ull << lane) - 1ull))] = rid[r];
-    nvalid += tot;
-  }
-  __syncthreads();
-  k.b = b;
-  k.nvalid = nvalid;
-  k.padded = padded;
-}
 
 // ---------------------------------------------------------------------------
 // shared epilogue
@@ -1317,3 +947,5 @@ extern "C" int sas_combine_v1(const SasCombineArgs* a, void* stream) {
   sas::clear_error();
   return combine_impl(a, (hipStream_t)stream);
 }
+
+}  // namespace sas
