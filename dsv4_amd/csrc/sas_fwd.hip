@@ -35,6 +35,13 @@
 
 #include "sas_kern.h"
 
+#ifndef SAS_PFK
+#define SAS_PFK 3   // K operand k-steps read ahead (32-row steps)
+#endif
+#ifndef SAS_PFV
+#define SAS_PFV 4   // V^T operand channel tiles read ahead (32-row steps)
+#endif
+
 namespace sas {
 namespace {
 
@@ -55,8 +62,8 @@ struct Cfg {
   static constexpr int NTL = kDV / 16 / CS;                 // 16-channel O tiles per wave
   // rows per step: 32, or 16 when 32-row slots would leave a ring shallower than 2
   static constexpr int TR = kLdsRows / (KW * 32) < 2 ? 16 : 32;
-  static constexpr int PFK = TR == 16 ? 4 : 3;              // K operand reads ahead
-  static constexpr int PFV = TR == 16 ? 8 : 4;              // V^T operand reads ahead
+  static constexpr int PFK = TR == 16 ? 4 : SAS_PFK;        // K operand reads ahead
+  static constexpr int PFV = TR == 16 ? 8 : SAS_PFV;        // V^T operand reads ahead
   static constexpr bool CH2 = true;                         // two QK^T accumulation chains
   static constexpr int MT = TR / 16;                        // 16-key tiles per step
   static constexpr int NST = kLdsRows / (KW * TR);          // ring depth per key-group
