@@ -121,7 +121,7 @@ struct Fwd {
       const int blk = (o * C::WK + jw) * 64;        // wave-uniform chunk base
       const int P = blk + lane;
       const int r = P / C::CH, pc = P - r * C::CH;
-      const int c = pc ^ swz(r);
+      const int c = pc ^ swz<C::CH>(r);
       const int id = r < nk ? lds_rows[rp + r] : dummy;
       dma16(row_ptr(id) + c * 16, __builtin_amdgcn_readfirstlane(lds_addr_of(&lds_ring[sl + blk])));
     }
@@ -156,7 +156,7 @@ struct Fwd {
       if (e >= C::TR * C::FCPR) continue;
       const int r = e / C::FCPR, c = e - r * C::FCPR;
       uint4* row = &lds_ring[sl + r * C::CH];
-      const int sw = swz(r);
+      const int sw = swz<C::CH>(r);
       if (c < 32) {
         const uint32_t w[4] = {fbuf[k].x, fbuf[k].y, fbuf[k].z, fbuf[k].w};
         uint32_t o[8];
@@ -182,14 +182,18 @@ struct Fwd {
     f32x4 sacc[MT], sodd[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) { sacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f}; sodd[mt] = sacc[mt]; }
-    // K operand: rows c16 and 16 + c16 share swz(); logical chunk 4ks + g only
-    // changes in its low 3 bits with ks & 1, the rest is an immediate offset.
-    // Reads run kPfK k-steps ahead of the MFMAs that consume them.
-    const int ksw = swz(c16);
+    // K operand: rows c16 and 16 + c16 share the swizzle; logical chunk
+    // 4ks + g lies in XOR group ks / KPG at offset qo[ks % KPG], the group
+    // base being an immediate offset. Reads run kPfK k-steps ahead of the
+    // MFMAs that consume them.
+    constexpr int SG = kSwzGroup<C::CH>, KPG = SG / 4;
+    const int ksw = swz<C::CH>(c16);
     const uint4* qrow = &lds_ring[sl + c16 * C::CH];
-    const int qo0 = g ^ ksw, qo1 = (4 + g) ^ ksw;
+    int qo[KPG];
+#pragma unroll
+    for (int j = 0; j < KPG; ++j) qo[j] = (4 * j + g) ^ ksw;
     auto kfrag = [&](int ks, int mt) {
-      return qrow[mt * 16 * C::CH + (ks >> 1) * 8 + ((ks & 1) ? qo1 : qo0)];
+      return qrow[mt * 16 * C::CH + (ks / KPG) * SG + qo[ks % KPG]];
     };
     constexpr int kPfK = C::PFK;
     uint4 af[kPfK][MT];
@@ -270,18 +274,19 @@ struct Fwd {
     // This wave's O tiles are channel tiles cs * NTL + mt, mt < NTL (their
     // chunks start cs * NTL * 2 chunks into the row).
     const int vr = 4 * g + (c16 >> 2);
-    const int vsw = swz(vr);
+    const int vsw = swz<C::CH>(vr);
     const int vb = (c16 & 3) >> 1;
     const char* vbase = reinterpret_cast<const char*>(&lds_ring[sl + vr * C::CH]) + (c16 & 1) * 8 +
-                        cs * (C::NTL / 4) * 128;
-    // logical chunk 2mt + vb: its low 3 bits cycle with mt & 3
-    int voff[4];
+                        cs * C::NTL * 32;
+    // logical chunk 2mt + vb lies in XOR group mt / TPG at voff[mt % TPG]
+    constexpr int TPG = kSwzGroup<C::CH> / 2;
+    int voff[TPG];
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) voff[q4] = ((2 * q4 + vb) ^ vsw) * 16;
+    for (int q = 0; q < TPG; ++q) voff[q] = ((2 * q + vb) ^ vsw) * 16;
     constexpr int kPfV = C::PFV;
     if constexpr (MT == 2) {
       auto vfrag = [&](int mt) {
-        const char* a0 = vbase + (mt >> 2) * 128 + voff[mt & 3];
+        const char* a0 = vbase + (mt / TPG) * TPG * 32 + voff[mt % TPG];
         const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a0));
         const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a0 + 16 * C::CH * 16));
         const uint2 u0 = __builtin_bit_cast(uint2, v0), u1 = __builtin_bit_cast(uint2, v1);
@@ -307,7 +312,7 @@ struct Fwd {
       // 16 keys: one transposed read per 16-channel tile, 16x16x16 MFMA whose
       // B operand (keys 4g..4g+3 of head c16) is exactly this lane's P
       auto vfrag = [&](int mt) {
-        const char* a0 = vbase + (mt >> 2) * 128 + voff[mt & 3];
+        const char* a0 = vbase + (mt / TPG) * TPG * 32 + voff[mt % TPG];
         return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a0)));
       };
       const uint2 pfrag = make_uint2(pk[0], pk[1]);
@@ -529,7 +534,10 @@ struct Dec {
   static constexpr int KS = D / 32;          // k-steps per row (chunks per lane)
   static constexpr int NP = 3;               // steps in flight per wave
   static constexpr int VCH = kDV / 8;        // chunks per V row
-  static constexpr int VT = 16 * VCH;        // chunks per V tile
+  // V tile row stride: 72 chunks, so the 8-chunk-group swizzle applies (a
+  // 16-chunk-group one costs the kernel its registers)
+  static constexpr int VRS = VCH + 8;
+  static constexpr int VT = 16 * VRS;        // chunks per V tile
   static constexpr int ROWB = KVF ? kRow656 : D * 2;
   static_assert(!KVF || D == 576, "fp8 rows carry 576 channels");
   static_assert(4 * VT <= kLdsRows * kChunksMax, "V tiles fit");
@@ -602,9 +610,9 @@ struct Dec {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = kchunk(st[J], ks);
     // V half -> this wave's LDS tile (row c16, chunk 4ks + g, swizzled)
-    const int vsw_w = swz(c16);
+    const int vsw_w = swz<VRS>(c16);
 #pragma unroll
-    for (int ks = 0; ks < VCH / 4; ++ks) lds_ring[vt + c16 * VCH + ((4 * ks + g) ^ vsw_w)] = kf[ks];
+    for (int ks = 0; ks < VCH / 4; ++ks) lds_ring[vt + c16 * VRS + (((4 * ks + g) & ~7) | (((4 * ks + g) & 7) ^ vsw_w))] = kf[ks];
     // S^T[16 keys x 16 heads] = K . Q^T, even / odd k-steps in two chains
     f32x4 se = f32x4{0.f, 0.f, 0.f, 0.f}, so = se;
 #pragma unroll
@@ -648,14 +656,15 @@ struct Dec {
     // O^T[512 x 16] += V^T . P^T: one transposed read per 16-channel tile
     // (rows 4g + c16/4, channels mt*16 + 4*(c16&3)), 16x16x16 MFMA
     const int vr = 4 * g + (c16 >> 2);
-    const int vsw = swz(vr);
+    const int vsw = swz<VRS>(vr);
     const int vb = (c16 & 3) >> 1;
-    const char* vbase = reinterpret_cast<const char*>(&lds_ring[vt + vr * VCH]) + (c16 & 1) * 8;
-    int voff[4];
+    const char* vbase = reinterpret_cast<const char*>(&lds_ring[vt + vr * VRS]) + (c16 & 1) * 8;
+    constexpr int TPG = kSwzGroup<VRS> / 2;
+    int voff[TPG];
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) voff[q4] = ((2 * q4 + vb) ^ vsw) * 16;
+    for (int q = 0; q < TPG; ++q) voff[q] = ((2 * q + vb) ^ vsw) * 16;
     auto vfrag = [&](int mt) {
-      const char* a0 = vbase + (mt >> 2) * 128 + voff[mt & 3];
+      const char* a0 = vbase + (mt / TPG) * TPG * 32 + voff[mt % TPG];
       return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a0)));
     };
     constexpr int kPf = 8;

@@ -122,11 +122,28 @@ __device__ __forceinline__ f32x4 mfma16k<_Float16>(const uint2& a, const uint2& 
                                                __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
 }
 
-// Chunk swizzle inside each aligned group of 8 chunks of a row: row r keeps
-// logical chunk c at position c ^ swz(r). With it, 8 lanes reading the same
-// chunk of rows r..r+7 (QK^T operand) and 16 lanes reading 4 rows x 2 chunks
-// (transposed PV operand) each touch distinct banks.
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// Row swizzle of 16-byte chunks for LDS tiles whose rows are RC chunks long:
+// row r keeps logical chunk c at c ^ swz<RC>(r). gfx950 LDS has 64 banks of
+// 4 bytes (a 256-byte period, 16 chunk positions). A ds_read_b128 serves each
+// half-wave in two cycles, one per set of 16 lanes whose lane-id bits 2..4
+// have equal parity; ds_read_b64_tr_b16 serves 32 lanes (256 bytes) per
+// cycle. The QK^T operand read (lane l: row l & 15 of a 16-row tile, logical
+// chunk 4 ks + l / 16) and the transposed PV read (lane l: row
+// 4 (l / 16) + (l & 15) / 4, chunks 2t, 2t + 1) then touch every bank once
+// per cycle.
+//  RC = 0 mod 16: XOR inside aligned 16-chunk groups with 2 (r & 7).
+//  RC = 8 mod 16: odd rows start half a period later, so XOR inside aligned
+//                 8-chunk groups with r & 6 (the last 8-chunk group of a
+//                 72-chunk row has no 16-chunk partner).
+template <int RC>
+__device__ __forceinline__ int swz(int r) {
+  static_assert(RC % 8 == 0, "rows of whole 8-chunk groups");
+  if constexpr (RC % 16 == 0) return (r & 7) << 1;
+  else return r & 6;
+}
+// chunks per aligned XOR group of swz<RC>
+template <int RC>
+inline constexpr int kSwzGroup = RC % 16 == 0 ? 16 : 8;
 
 // 16 bytes per lane global -> LDS (lane i lands at lds_addr + 16 i). Issued
 // as inline asm so the compiler does not track it: its LDS-DMA tracking
