@@ -1,30 +1,30 @@
 // sparse_attn_sharedkv forward for MI355X (gfx950 / CDNA4).
 //
-// One workgroup of 4 waves per (query token, head group, KV split). The
-// token's key slots are the sliding window (win_left + 1 slots) followed by
-// the top-k compressed entries (or the dense compressed prefix for CFA).
+// One workgroup per (query token, head group, KV split); NW = 4 or 8 waves.
+// The token's key slots are the sliding window (win_left + 1 slots) followed
+// by the top-k compressed entries (or the dense compressed prefix for CFA).
 //
-//  1. Resolve the workgroup's slot range to physical cache rows through the
-//     block tables, drop masked slots (window band, idx < 0, idx >= causal
-//     threshold) and compact the survivors, in order, into LDS. The batch of
-//     the token comes from one ballot over q_prefix; the top-k indices, the
-//     batch scalars and the query load in one round trip, the block tables in
-//     a second one.
-//  2. The 4 waves form HW head-waves x KW key-groups (HW * KW = 4). A wave
-//     owns 16 query heads; a key-group owns a contiguous share of the rows and
+//  1. Resolve the workgroup's slot range to cache rows through the block
+//     tables, drop masked slots (window band, idx < 0, idx >= causal
+//     threshold) and compact the survivors' row addresses, in order, into LDS
+//     (resolve() in sas_kern.h: two global round trips).
+//  2. The waves form HW head-waves (16 query heads each) x CS channel halves x
+//     KW key-groups. A key-group owns a contiguous share of the rows and
 //     streams it in steps of TR rows (32, or 16 when every wave is its own
 //     key-group) through a ring of LDS slots. Rows move HBM -> LDS with
-//     global_load_lds_dwordx4 (no register staging), stored row-major with an
-//     XOR swizzle of 16-byte chunks so both operand reads below are
-//     bank-conflict free. fp8 rows go through registers instead (dequantised
-//     to bf16 on the way). With HW = 1 the waves share nothing until the
-//     epilogue, so the step loop has no workgroup barrier.
+//     global_load_lds_dwordx4 (no register staging), issued between the QK^T
+//     MFMAs of the step before, into the slot that step freed; one workgroup
+//     barrier per step. Tiles are row-major with an XOR swizzle of 16-byte
+//     chunks that keeps both operand reads below bank-conflict free. fp8 rows
+//     go through registers instead (dequantised to bf16 on the way). With
+//     one wave per key-group the step loop has no workgroup barrier.
 //  3. Per step and wave:  S^T[TR keys x 16 heads] = K . Q^T  (16x16x32 MFMA,
 //     A from LDS, Q^T resident in VGPRs), sink-seeded online softmax in the
 //     log2 domain, P rounded to the query dtype, then
-//     O^T[512 x 16 heads] += V^T . P^T where the V^T operand comes straight
-//     from the row-major tile with ds_read_b64_tr_b16 and P^T is already in
-//     the register layout the MFMA wants (the S^T accumulator layout).
+//     O^T[channels x 16 heads] += V^T . P^T where the V^T operand comes
+//     straight from the row-major tile with ds_read_b64_tr_b16 and P^T is
+//     already in the register layout the MFMA wants (the S^T accumulator
+//     layout).
 //  4. Key-groups merge through LDS (max / sum rescale); the result is the
 //     output + LSE, or with several KV splits an unnormalised fp32 partial
 //     that the LSE combine kernel merges with the sink.
@@ -91,7 +91,7 @@ struct Fwd {
   int rbeg;            // this key-group's first row in lds_rows
   int ring;           // chunk offset of this key-group's NST slots in lds_ring
   int nrows;           // rows this key-group owns
-  int nsteps, nsteps_max, dummy;
+  int nsteps, nsteps_max;
   uint4 qf[C::KS];
   float m_run, l_run;
   f32x4 acc[C::NTL];
@@ -105,26 +105,42 @@ struct Fwd {
         cs((wave % C::WK) / HW), jw(wave % C::WK), gt((wave % C::WK) * 64 + lane_),
         nops((C::NI - wave % C::WK + C::WK - 1) / C::WK) {}
 
-  __device__ __forceinline__ const uint8_t* row_ptr(int id) const {
-    return id >= 0 ? p.ori_kv + (size_t)id * C::ROWB : p.cmp_kv + (size_t)(-id - 2) * C::ROWB;
-  }
   __device__ __forceinline__ int slot(int j) const { return ring + j * C::SLOT; }
 
   // -- bf16 / fp16 rows: DMA one step into slot j ------------------------------
-  __device__ __forceinline__ void issue(int j, int step) {
-    const int sl = slot(j);
+  // Lane `lane` of the wave's o-th instruction of a step moves row drow(o) of
+  // the step, logical chunk pc ^ swz(row) (byte offset dcol(o)) to slot chunk
+  // (o * WK + jw) * 64 + lane. The row addresses are read from LDS for all of
+  // the wave's instructions first, so one LDS wait covers them (the DMA asm
+  // is a memory barrier to the compiler). Rows past the end of the last step
+  // repeat its last row: they are masked out of the softmax, and a real row
+  // keeps P.V finite.
+  __device__ __forceinline__ int drow(int o) const { return ((o * C::WK + jw) * 64 + lane) / C::CH; }
+  __device__ __forceinline__ uint32_t dcol(int o) const {
+    const int P = (o * C::WK + jw) * 64 + lane, r = P / C::CH;
+    return (uint32_t)(((P - r * C::CH) ^ swz<C::CH>(r)) * 16);
+  }
+  struct Dma {
+    uint64_t ra[C::OPS];   // row address of each of the wave's instructions
+    uint32_t lds;          // LDS byte address of the slot
+  };
+  __device__ __forceinline__ void prep(Dma& d, int j, int step) const {
     const int rp = rbeg + step * C::TR;
-    const int nk = min(C::TR, nrows - step * C::TR);
+    const int last = rp + min(C::TR, nrows - step * C::TR) - 1;   // nk >= 1 for every issued step
 #pragma unroll
-    for (int o = 0; o < C::OPS; ++o) {
-      if (C::NI % C::WK && o * C::WK + jw >= C::NI) break;   // wave-uniform
-      const int blk = (o * C::WK + jw) * 64;        // wave-uniform chunk base
-      const int P = blk + lane;
-      const int r = P / C::CH, pc = P - r * C::CH;
-      const int c = pc ^ swz<C::CH>(r);
-      const int id = r < nk ? lds_rows[rp + r] : dummy;
-      dma16(row_ptr(id) + c * 16, __builtin_amdgcn_readfirstlane(lds_addr_of(&lds_ring[sl + blk])));
-    }
+    for (int o = 0; o < C::OPS; ++o) d.ra[o] = lds_rows[min(rp + drow(o), last)];
+    d.lds = lds_addr_of(&lds_ring[slot(j)]);
+  }
+  __device__ __forceinline__ void fire(const Dma& d, int o) const {
+    if (C::NI % C::WK && o * C::WK + jw >= C::NI) return;   // wave-uniform
+    dma16(reinterpret_cast<const void*>(d.ra[o] + dcol(o)),
+          __builtin_amdgcn_readfirstlane(d.lds + (o * C::WK + jw) * 64 * 16));
+  }
+  __device__ __forceinline__ void issue(int j, int step) {
+    Dma d;
+    prep(d, j, step);
+#pragma unroll
+    for (int o = 0; o < C::OPS; ++o) fire(d, o);
   }
 
   // -- fp8 rows: global -> registers, dequantised into a slot on store -------
@@ -138,7 +154,7 @@ struct Fwd {
       fbuf[k] = make_uint4(0, 0, 0, 0);
       fsc[k] = 0.f;
       if (e < C::TR * C::FCPR && r < nk) {
-        const uint8_t* src = row_ptr(lds_rows[rp + r]);
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(lds_rows[rp + r]);
         if (c < 32) {
           fbuf[k] = *reinterpret_cast<const uint4*>(src + c * 16);
           fsc[k] = *reinterpret_cast<const float*>(src + 512 + 4 * (c >> 3));
@@ -176,7 +192,11 @@ struct Fwd {
   }
 
   // -- one step of attention (TR keys) for this wave's 16 heads --------------
-  __device__ __forceinline__ void compute(int sl, int step) {
+  // dma(o), o < OPS, issues the wave's o-th DMA instruction of a later step;
+  // the calls are spread over the QK^T k-steps so the vector memory pipe
+  // works while the MFMAs run.
+  template <typename DmaFn>
+  __device__ __forceinline__ void compute(int sl, int step, DmaFn&& dma) {
     constexpr int MT = C::MT;
     const int nk = min(C::TR, nrows - step * C::TR);
     f32x4 sacc[MT], sodd[MT];
@@ -216,7 +236,10 @@ struct Fwd {
         if (C::CH2 && (ks & 1)) sodd[mt] = mfma32k<QT>(a[mt], qf[ks], sodd[mt]);
         else sacc[mt] = mfma32k<QT>(a[mt], qf[ks], sacc[mt]);
       }
+      if ((ks & 1) && ks / 2 < C::OPS) dma(ks / 2);
     }
+#pragma unroll
+    for (int o = C::KS / 2; o < C::OPS; ++o) dma(o);
     // schedule: the prefetch reads first, then per k-step MT MFMAs + MT reads
     __builtin_amdgcn_sched_group_barrier(0x100, MT * kPfK, 0);
 #pragma unroll
@@ -239,8 +262,7 @@ struct Fwd {
         sv[mt][j] = x;
         mloc = fmaxf(mloc, x);
       }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    mloc = rows_max(mloc);
     // Lazy rescale: m_run is a reference max, moved (and O, l rescaled) only
     // when some head's max rises more than kLazyLog2 above it, so P <= 2^8.
     // out = acc / l and lse = m_run + log2 l are exact for any reference.
@@ -265,8 +287,7 @@ struct Fwd {
       pk[mt * 2 + 0] = to_bits<QT>(pv[0]) | (to_bits<QT>(pv[1]) << 16);
       pk[mt * 2 + 1] = to_bits<QT>(pv[2]) | (to_bits<QT>(pv[3]) << 16);
     }
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
+    lsum = rows_sum(lsum);
     l_run += lsum;
     // V^T operand by transposed reads: lanes of group g address rows
     // 4g + c16/4 (and +16), channels mt*16 + 4*(c16&3); each lane receives
@@ -349,24 +370,29 @@ struct Fwd {
     const int it = it0 + J;
     if (it >= nsteps_max) return;   // uniform over the workgroup (HW > 1) / wave
     if constexpr (!KVF) {
-      // my DMA for step `it` done (steps after it may still stream), then all waves
-      const int after = it < nsteps ? min(C::NST - 1, nsteps - 1 - it) : 0;
+      // Steps up to it + NST - 2 have been issued. My DMA for step `it` done
+      // (the later ones may still stream), then all waves: every wave has
+      // finished step it - 1, so its slot (J + NST - 1) % NST takes step
+      // it + NST - 1 while step it computes.
+      const int after = it < nsteps ? min(C::NST - 2, nsteps - 1 - it) : 0;
       if constexpr (C::NI % C::WK) {
         wait_vm_rt(max(after, 0) * nops);
       } else {
         if (after <= 0) wait_vm<0>();
         else if (after == 1) wait_vm<C::OPS>();
-        else if (after == 2) wait_vm<(C::NST > 2 ? 2 * C::OPS : 0)>();
-        else wait_vm<(C::NST > 3 ? 3 * C::OPS : 0)>();
+        else wait_vm<(C::NST > 3 ? 2 * C::OPS : 0)>();
       }
       step_sync();
-      if (it < nsteps) compute(slot(J), it);
-      step_sync();
-      if (it + C::NST < nsteps) issue(J, it + C::NST);
+      if (it < nsteps) {
+        const bool more = it + C::NST - 1 < nsteps;
+        Dma d;
+        if (more) prep(d, (J + C::NST - 1) % C::NST, it + C::NST - 1);
+        compute(slot(J), it, [&](int o) { if (more) fire(d, o); });
+      }
     } else {
       // fp8: registers hold step it+1; slot J holds step it
       step_sync();
-      if (it < nsteps) compute(slot(J), it);
+      if (it < nsteps) compute(slot(J), it, [](int) {});
       if (it + 1 < nsteps) fstore((J + 1) % C::NST);
       if (it + 2 < nsteps) fload(it + 2);
     }
@@ -375,7 +401,7 @@ struct Fwd {
   __device__ __forceinline__ void run() {
     if constexpr (!KVF) {
 #pragma unroll
-      for (int j = 0; j < C::NST; ++j)
+      for (int j = 0; j < C::NST - 1; ++j)
         if (j < nsteps) issue(j, j);
     } else {
       if (nsteps > 0) { fload(0); fstore(0); }
@@ -479,14 +505,14 @@ __global__ void __launch_bounds__(NW * 64)
 sas_fwd_kernel(const FwdParams p) {
   using C = Cfg<HW, NW, D, QT, KVF>;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int item = (int)(blockIdx.x % kXcds) * p.per_xcd + (int)(blockIdx.x / kXcds);
-  if (item >= p.items) return;
-  Tok k = item_of(p);
+  const int item = item_index(p);
+  if (item < 0) return;
+  Tok k = item_of(p, item);
   Fwd<HW, NW, D, QT, KVF> f(p, lane, wave);
   const int hq = k.hg * (16 * HW) + f.hw * 16 + f.c16;
   // Q^T operand in registers (head hq, channels ks*32 + 8g .. +8), loaded
   // behind the block-table reads of the slot resolution
-  resolve<NW * 64>(p, k, tid, lane, wave, [&] {
+  resolve<NW * 64, C::ROWB>(p, k, tid, lane, wave, [&] {
     const uint4* qp = reinterpret_cast<const uint4*>(p.q + ((size_t)k.t * p.H + hq) * D * 2);
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) f.qf[ks] = qp[ks * 4 + f.g];
@@ -501,7 +527,6 @@ sas_fwd_kernel(const FwdParams p) {
   f.nrows = min(nvalid, gbeg + per) - gbeg;
   f.nsteps = (f.nrows + C::TR - 1) / C::TR;
   f.nsteps_max = per / C::TR;
-  f.dummy = nvalid > 0 ? lds_rows[0] : 0;
 
   // retire every load the compiler tracks (Q, tables, indices) before the
   // DMA ring starts, so none of its own vmcnt waits lands inside the loop
@@ -550,16 +575,14 @@ struct Dec {
 
   const FwdParams& p;
   const int lane, c16, g;
-  int rbeg, nrows, nsteps, dummy, vt;
+  int rbeg, nrows, nsteps, vt;
+  uint64_t dummy;
   uint4 qf[KS];
   float m_run, l_run;
   f32x4 acc[kDV / 16];
 
   __device__ Dec(const FwdParams& p_, int lane_) : p(p_), lane(lane_), c16(lane_ & 15), g(lane_ >> 4) {}
 
-  __device__ __forceinline__ const uint8_t* row_ptr(int id) const {
-    return id >= 0 ? p.ori_kv + (size_t)id * ROWB : p.cmp_kv + (size_t)(-id - 2) * ROWB;
-  }
 
   // Step `step` of this wave into a stage. Loads are issued for every stage
   // unconditionally, so the compiler's vmcnt bookkeeping sees the same load
@@ -568,8 +591,8 @@ struct Dec {
   __device__ __forceinline__ void load(Stage& st, int step) const {
     const int i = step * 16 + c16;
     const bool live = step < nsteps;
-    const int id = lds_rows[rbeg + min(i, max(nrows - 1, 0))];
-    const uint8_t* src = row_ptr(live && i < nrows ? id : dummy);
+    const uint64_t ra = lds_rows[rbeg + min(i, max(nrows - 1, 0))];
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(live && i < nrows ? ra : dummy);
     const int gm = live ? g : 0, lm = live ? 1 : 0;
     if constexpr (!KVF) {
 #pragma unroll
@@ -702,11 +725,11 @@ __global__ void __launch_bounds__(256)
 sas_dec_kernel(const FwdParams p) {
   using C = Dec<D, QT, KVF>;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int item = (int)(blockIdx.x % kXcds) * p.per_xcd + (int)(blockIdx.x / kXcds);
-  if (item >= p.items) return;
-  Tok k = item_of(p);
+  const int item = item_index(p);
+  if (item < 0) return;
+  Tok k = item_of(p, item);
   C f(p, lane);
-  resolve<256>(p, k, tid, lane, wave, [] {});
+  resolve<256, C::ROWB>(p, k, tid, lane, wave, [] {});
   const int nvalid = k.nvalid;
   const int hq = k.hg * 16 + f.c16;
   // key-group share of wave `wave`: whole 16-row steps, wave 0 first
@@ -715,7 +738,7 @@ sas_dec_kernel(const FwdParams p) {
   f.rbeg = gbeg;
   f.nrows = min(nvalid, gbeg + per) - gbeg;
   f.nsteps = (f.nrows + 15) >> 4;
-  f.dummy = nvalid > 0 ? lds_rows[0] : 0;
+  f.dummy = nvalid > 0 ? lds_rows[0] : reinterpret_cast<uint64_t>(p.ori_kv);
   f.vt = wave * C::VT;
   // Q^T operand in registers (head hq, channels ks*32 + 8g .. +8), ahead of
   // the first K loads
@@ -947,9 +970,8 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   fp.cmp_ratio = std::max(1, a->cmp_ratio); fp.win_left = a->win_left;
   fp.scale_log2 = a->softmax_scale * kLog2e;
   fp.nsplit = pl.nsplit; fp.slots_per_split = pl.sps; fp.nhg = pl.nhg;
-  fp.items = (int)(a->T * pl.nhg * pl.nsplit);
-  fp.per_xcd = (fp.items + kXcds - 1) / kXcds;
-  const int nblocks = fp.per_xcd * kXcds;
+  // item_index(): ceil(T / 8) tokens per XCD, nhg * nsplit workgroups each
+  const int nblocks = (int)((a->T + kXcds - 1) / kXcds) * pl.nhg * pl.nsplit * kXcds;
   hipStream_t st = (hipStream_t)stream;
 
   if (fp8) rc = dispatch_hw<576, __bf16, 1>(pl.hw, pl.nw, fp, nblocks, st);

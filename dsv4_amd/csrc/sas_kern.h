@@ -38,7 +38,8 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 static __shared__ __attribute__((aligned(16))) uint4 lds_ring[kLdsRows * kChunksMax];  // 147,456 B
-static __shared__ int lds_rows[kMaxSlots];
+// compacted rows of the workgroup: the byte address of each cache row
+static __shared__ uint64_t lds_rows[kMaxSlots];
 static __shared__ int lds_cnt[kRoundsMax][kMaxWaves];
 static __shared__ float lds_ml[kMaxWaves][2][16];
 
@@ -62,7 +63,7 @@ struct FwdParams {
   int cmp_bs, cmp_bt_stride, cmp_nblocks;
   int K, scenario, cmp_ratio, win_left;
   float scale_log2;
-  int nsplit, slots_per_split, nhg, items, per_xcd;
+  int nsplit, slots_per_split, nhg;
 };
 
 // ---------------------------------------------------------------------------
@@ -144,6 +145,22 @@ __device__ __forceinline__ int swz(int r) {
 // chunks per aligned XOR group of swz<RC>
 template <int RC>
 inline constexpr int kSwzGroup = RC % 16 == 0 ? 16 : 8;
+
+// Max / sum over the 4 rows (16-lane groups) of a wave, leaving the result in
+// every lane: v_permlane16_swap / v_permlane32_swap exchange rows inside the
+// VALU (no LDS round trip as a ds_bpermute-based shuffle would take).
+__device__ __forceinline__ float rows_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float m = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 // 16 bytes per lane global -> LDS (lane i lands at lds_addr + 16 i). Issued
 // as inline asm so the compiler does not track it: its LDS-DMA tracking
@@ -253,14 +270,24 @@ __device__ __forceinline__ void merge_partials(const FwdParams& p, int t, int h0
 
 struct Tok {
   int t, hg, sp;     // token, head group, KV split
-  int b, nvalid;     // batch, compacted rows in lds_rows
+  int b, nvalid;     // batch, compacted row addresses in lds_rows
   bool padded;       // (b, position) outside the batch's query length
 };
 
-__device__ __forceinline__ Tok item_of(const FwdParams& p) {
-  // XCD-aware item mapping: XCD x = blockIdx % 8 owns a contiguous item range,
-  // so all splits / head groups of a token (and neighbouring tokens) share L2.
-  const int item = (int)(blockIdx.x % kXcds) * p.per_xcd + (int)(blockIdx.x / kXcds);
+// Work item of this workgroup, or -1 for a padding workgroup. Tokens are
+// dealt round-robin to the 8 XCDs (blockIdx % 8 is the XCD), latest token
+// first; all head groups and splits of a token go to one XCD and share its
+// L2. Every XCD then gets the same mix of long and short token rows (causal
+// prefill: rows grow with the position), and the longest items start first.
+__device__ __forceinline__ int item_index(const FwdParams& p) {
+  const int x = (int)(blockIdx.x % kXcds), l = (int)(blockIdx.x / kXcds);
+  const int per_tok = p.nhg * p.nsplit;
+  const int q = l / per_tok, sub = l - q * per_tok;
+  const int t = p.T - 1 - (q * kXcds + x);
+  return t >= 0 ? t * per_tok + sub : -1;
+}
+
+__device__ __forceinline__ Tok item_of(const FwdParams& p, int item) {
   Tok k;
   const int per_tok = p.nhg * p.nsplit;
   k.t = item / per_tok;
@@ -271,10 +298,11 @@ __device__ __forceinline__ Tok item_of(const FwdParams& p) {
 }
 
 // Resolve the item's slot range to cache rows and compact the valid ones, in
-// slot order, into lds_rows[0, nvalid). Raw rows are stored as id >= 0,
-// compressed rows as -(id + 2). `mid` runs after the block-table loads are
-// issued (a caller can put its own loads behind them there).
-template <int NT, typename Mid>
+// slot order, into lds_rows[0, nvalid) as row byte addresses (ROWB bytes per
+// row), so the streaming loops only add a chunk offset. `mid` runs after the
+// block-table loads are issued (a caller can put its own loads behind them
+// there).
+template <int NT, int ROWB, typename Mid>
 __device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int lane, int wave, Mid&& mid) {
   constexpr int NWV = NT / 64;
   constexpr int kRounds = (kMaxSlots + NT - 1) / NT;
@@ -324,7 +352,8 @@ __device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int
   // Every table read is issued unconditionally at a clamped, in-range
   // address (validity is kept apart), so the reads of all rounds are in
   // flight together and retire with one wait.
-  int rid[kRounds];
+  uint64_t rad[kRounds];
+  bool val[kRounds];
   {
     const int32_t* obt = p.ori_bt + (size_t)b * p.ori_bt_stride;
     const int32_t* cbt = p.cmp_bt ? p.cmp_bt + (size_t)b * p.cmp_bt_stride : obt;
@@ -359,19 +388,17 @@ __device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) {
-      rid[r] = -1;
-      if (ori[r]) {
-        if (ok[r] && phys[r] >= 0 && phys[r] < p.ori_nblocks) rid[r] = phys[r] * p.ori_bs + off[r];
-      } else {
-        if (ok[r] && phys[r] >= 0 && phys[r] < p.cmp_nblocks) rid[r] = -(phys[r] * p.cmp_bs + off[r] + 2);
-      }
+      const bool inb = phys[r] >= 0 && phys[r] < (ori[r] ? p.ori_nblocks : p.cmp_nblocks);
+      val[r] = ok[r] && inb;
+      const int row = val[r] ? phys[r] * (ori[r] ? p.ori_bs : p.cmp_bs) + off[r] : 0;
+      rad[r] = reinterpret_cast<uint64_t>(ori[r] ? p.ori_kv : p.cmp_kv) + (uint64_t)(uint32_t)row * ROWB;
     }
   }
   // ---- compaction (ballot + per-wave counts) -------------------------------
   uint64_t vmask[kRounds];
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
-    vmask[r] = __ballot(rid[r] != -1);
+    vmask[r] = __ballot(val[r]);
     if (r < nr && lane == 0) lds_cnt[r][wave] = __popcll(vmask[r]);
   }
   __syncthreads();
@@ -386,8 +413,8 @@ __device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int
       wpre += w < wave ? cw : 0;
       tot += cw;
     }
-    if (rid[r] != -1)
-      lds_rows[nvalid + wpre + __popcll(vmask[r] & ((1ull << lane) - 1ull))] = rid[r];
+    if (val[r])
+      lds_rows[nvalid + wpre + __popcll(vmask[r] & ((1ull << lane) - 1ull))] = rad[r];
     nvalid += tot;
   }
   __syncthreads();
