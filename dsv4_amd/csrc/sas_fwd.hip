@@ -60,16 +60,23 @@ struct Cfg {
   static constexpr int WK = HW * CS;                        // waves sharing a key-group's slots
   static constexpr int KW = NW / WK;
   static constexpr int NTL = kDV / 16 / CS;                 // 16-channel O tiles per wave
+  // With two channel halves the QK^T k-steps are split as well: each wave of
+  // a pair sums S over its half of the D channels and the pair adds the two
+  // halves through LDS (no QK^T work is duplicated). The exchange buffer
+  // takes the ring rows above kRingRows.
+  static constexpr bool QS = CS == 2 && !KVF;
+  static constexpr int kRingRows = QS ? 96 : kLdsRows;
   // rows per step: 32, or 16 when 32-row slots would leave a ring shallower than 2
-  static constexpr int TR = kLdsRows / (KW * 32) < 2 ? 16 : 32;
+  static constexpr int TR = kRingRows / (KW * 32) < 2 ? 16 : 32;
   static constexpr int PFK = TR == 16 ? 4 : SAS_PFK;        // K operand reads ahead
   static constexpr int PFV = TR == 16 ? 8 : SAS_PFV;        // V^T operand reads ahead
   static constexpr bool CH2 = true;                         // two QK^T accumulation chains
   static constexpr int MT = TR / 16;                        // 16-key tiles per step
-  static constexpr int NST = kLdsRows / (KW * TR);          // ring depth per key-group
+  static constexpr int NST = kRingRows / (KW * TR) > 4 ? 4 : kRingRows / (KW * TR);   // ring depth per key-group
   static constexpr int SLOT = TR * kChunksMax;              // slot stride (chunks)
   static constexpr int CH = D / 8;                          // 16-byte chunks per bf16 row
   static constexpr int KS = D / 32;                         // QK^T k-steps
+  static constexpr int KSQ = QS ? KS / 2 : KS;              // k-steps of one wave
   static constexpr int GT = WK * 64;                        // threads per key-group
   static constexpr int NI = TR * CH / 64;                   // DMA instructions per step
   static constexpr int OPS = (NI + WK - 1) / WK;            // most DMA ops per wave per step
@@ -80,7 +87,9 @@ struct Cfg {
   static_assert(TR * CH % 64 == 0, "whole DMA instructions");
   static_assert(NST >= 2 && NST <= 4, "ring depth");
   static_assert((NST - 1) * OPS < 64, "vmcnt range");
-  static_assert(KW * NST * SLOT <= kLdsRows * kChunksMax, "ring fits");
+  static_assert(KW * NST * SLOT <= kRingRows * kChunksMax, "ring fits");
+  static_assert(!QS || (KS % 2 == 0 && NW * 64 * MT * 4 * 4 <= (kLdsRows - kRingRows) * kChunksMax * 16),
+                "S exchange fits above the ring");
 };
 
 template <int HW, int NW, int D, typename QT, int KVF>
@@ -92,7 +101,7 @@ struct Fwd {
   int ring;           // chunk offset of this key-group's NST slots in lds_ring
   int nrows;           // rows this key-group owns
   int nsteps, nsteps_max;
-  uint4 qf[C::KS];
+  uint4 qf[C::KSQ];
   float m_run, l_run;
   f32x4 acc[C::NTL];
   uint4 fbuf[KVF ? C::FOPS : 1];
@@ -192,26 +201,34 @@ struct Fwd {
   }
 
   // -- one step of attention (TR keys) for this wave's 16 heads --------------
-  // dma(o), o < OPS, issues the wave's o-th DMA instruction of a later step;
-  // the calls are spread over the QK^T k-steps so the vector memory pipe
-  // works while the MFMAs run.
-  template <typename DmaFn>
-  __device__ __forceinline__ void compute(int sl, int step, DmaFn&& dma) {
+  // qk: S^T of the step in slot sl as two accumulation chains (even / odd
+  // k-steps). dma(o), o < OPS, issues the wave's o-th DMA instruction of a
+  // later step; the calls are spread over the k-steps so the vector memory
+  // pipe works while the MFMAs run.
+  // mid(ks), with kMid set, puts VALU work of another step between the
+  // k-steps (the MFMAs of this step overlap it).
+  template <bool kMid = false, typename DmaFn, typename MidFn = void (*)(int)>
+  __device__ __forceinline__ void qk(int sl, f32x4 (&sacc)[C::MT], f32x4 (&sodd)[C::MT], DmaFn&& dma,
+                                     MidFn&& mid = [](int) {}) {
     constexpr int MT = C::MT;
-    const int nk = min(C::TR, nrows - step * C::TR);
-    f32x4 sacc[MT], sodd[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) { sacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f}; sodd[mt] = sacc[mt]; }
     // K operand: rows c16 and 16 + c16 share the swizzle; logical chunk
     // 4ks + g lies in XOR group ks / KPG at offset qo[ks % KPG], the group
     // base being an immediate offset. Reads run kPfK k-steps ahead of the
     // MFMAs that consume them.
+    // This wave's k-steps are cs * KSQ + ks, ks < KSQ; logical chunk L sits
+    // at (L & -SG) | ((L & (SG - 1)) ^ swz), and k-step ks + KPG one group
+    // (SG chunks) after k-step ks.
     constexpr int SG = kSwzGroup<C::CH>, KPG = SG / 4;
     const int ksw = swz<C::CH>(c16);
     const uint4* qrow = &lds_ring[sl + c16 * C::CH];
     int qo[KPG];
 #pragma unroll
-    for (int j = 0; j < KPG; ++j) qo[j] = (4 * j + g) ^ ksw;
+    for (int j = 0; j < KPG; ++j) {
+      const int L = 4 * ((C::QS ? cs * C::KSQ : 0) + j) + g;
+      qo[j] = (L & -SG) | ((L & (SG - 1)) ^ ksw);
+    }
     auto kfrag = [&](int ks, int mt) {
       return qrow[mt * 16 * C::CH + (ks / KPG) * SG + qo[ks % KPG]];
     };
@@ -223,11 +240,11 @@ struct Fwd {
       for (int mt = 0; mt < MT; ++mt) af[i][mt] = kfrag(i, mt);
     // even / odd k-steps accumulate separately: 2 MT independent MFMA chains
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
+    for (int ks = 0; ks < C::KSQ; ++ks) {
       uint4 a[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) a[mt] = af[ks % kPfK][mt];
-      if (ks + kPfK < C::KS) {
+      if (ks + kPfK < C::KSQ) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) af[ks % kPfK][mt] = kfrag(ks + kPfK, mt);
       }
@@ -237,21 +254,34 @@ struct Fwd {
         else sacc[mt] = mfma32k<QT>(a[mt], qf[ks], sacc[mt]);
       }
       if ((ks & 1) && ks / 2 < C::OPS) dma(ks / 2);
+      if constexpr (kMid) mid(ks);
     }
 #pragma unroll
-    for (int o = C::KS / 2; o < C::OPS; ++o) dma(o);
+    for (int o = C::KSQ / 2; o < C::OPS; ++o) dma(o);
     // schedule: the prefetch reads first, then per k-step MT MFMAs + MT reads
+    // (+ a share of the other step's VALU work)
     __builtin_amdgcn_sched_group_barrier(0x100, MT * kPfK, 0);
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
+    for (int ks = 0; ks < C::KSQ; ++ks) {
       __builtin_amdgcn_sched_group_barrier(0x008, MT, 0);
-      if (ks + kPfK < C::KS) __builtin_amdgcn_sched_group_barrier(0x100, MT, 0);
+      if (ks + kPfK < C::KSQ) __builtin_amdgcn_sched_group_barrier(0x100, MT, 0);
+      if constexpr (kMid) __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
     }
+  }
+
+  // smax: mask, scale and sink-seeded online softmax of a finished S^T; P
+  // rounded to the query dtype in the PV B-operand layout (pk), O and l
+  // rescaled when the reference max moves.
+  // smax_a: scaled, masked scores sv and the rescale; smax_b(e) for e in
+  // [0, MT * 4 + 2): exp of score e, then the packing of P, then the sum.
+  __device__ __forceinline__ void smax_a(f32x4 (&sacc)[C::MT], const f32x4 (&sodd)[C::MT], int step,
+                                         float (&sv)[C::MT][4]) {
+    constexpr int MT = C::MT;
+    const int nk = min(C::TR, nrows - step * C::TR);
     if constexpr (C::CH2) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) sacc[mt] += sodd[mt];
     }
-    float sv[MT][4];
     float mloc = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -274,21 +304,37 @@ struct Fwd {
 #pragma unroll
       for (int i = 0; i < C::NTL; ++i) acc[i] *= alpha;
     }
-    float lsum = 0.f;
-    uint32_t pk[2 * MT];
+  }
+  static constexpr int kSmaxB = C::MT * 4 + 2;
+  __device__ __forceinline__ void smax_b(int e, float (&sv)[C::MT][4], float& lsum, uint32_t (&pk)[2 * C::MT]) {
+    constexpr int MT = C::MT;
+    if (e < MT * 4) {
+      float& x = sv[e / 4][e % 4];
+      x = exp2f(x - m_run);
+      lsum = e == 0 ? x : lsum + x;
+    } else if (e == MT * 4) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float pv[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pv[j] = exp2f(sv[mt][j] - m_run);
-        lsum += pv[j];
+      for (int mt = 0; mt < MT; ++mt) {
+        pk[mt * 2 + 0] = to_bits<QT>(sv[mt][0]) | (to_bits<QT>(sv[mt][1]) << 16);
+        pk[mt * 2 + 1] = to_bits<QT>(sv[mt][2]) | (to_bits<QT>(sv[mt][3]) << 16);
       }
-      pk[mt * 2 + 0] = to_bits<QT>(pv[0]) | (to_bits<QT>(pv[1]) << 16);
-      pk[mt * 2 + 1] = to_bits<QT>(pv[2]) | (to_bits<QT>(pv[3]) << 16);
+    } else {
+      l_run += rows_sum(lsum);
     }
-    lsum = rows_sum(lsum);
-    l_run += lsum;
+  }
+  __device__ __forceinline__ void smax(f32x4 (&sacc)[C::MT], const f32x4 (&sodd)[C::MT], int step,
+                                       uint32_t (&pk)[2 * C::MT]) {
+    float sv[C::MT][4], lsum = 0.f;
+    smax_a(sacc, sodd, step, sv);
+#pragma unroll
+    for (int e = 0; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
+  }
+
+  // pv: O^T += V^T . P^T for the step in slot sl; dma(o) as in qk, spread
+  // over the channel tiles.
+  template <typename DmaFn>
+  __device__ __forceinline__ void pv(int sl, const uint32_t (&pk)[2 * C::MT], DmaFn&& dma) {
+    constexpr int MT = C::MT;
     // V^T operand by transposed reads: lanes of group g address rows
     // 4g + c16/4 (and +16), channels mt*16 + 4*(c16&3); each lane receives
     // 4 keys of channel mt*16 + c16. Reads run kPfV channel tiles ahead.
@@ -322,7 +368,10 @@ struct Fwd {
         const uint4 a = vf[mt % kPfV];
         if (mt + kPfV < C::NTL) vf[mt % kPfV] = vfrag(mt + kPfV);
         acc[mt] = mfma32k<QT>(a, pfrag, acc[mt]);
+        if (mt % 3 == 2 && mt / 3 < C::OPS) dma(mt / 3);
       }
+#pragma unroll
+      for (int o = C::NTL / 3; o < C::OPS; ++o) dma(o);
       __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPfV, 1);
 #pragma unroll
       for (int mt = 0; mt < C::NTL; ++mt) {
@@ -353,6 +402,42 @@ struct Fwd {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
         if (mt + kPf < C::NTL) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
       }
+#pragma unroll
+      for (int o = 0; o < C::OPS; ++o) dma(o);
+    }
+  }
+
+  // One step. With QS the two halves of S meet in LDS (one barrier, taken by
+  // every wave of the workgroup whether or not its key-group has the step).
+  template <typename DmaFn>
+  __device__ __forceinline__ void compute(int sl, int step, DmaFn&& dma) {
+    f32x4 sacc[C::MT], sodd[C::MT];
+    uint32_t pk[2 * C::MT];
+    const bool live = step < nsteps;
+    if (live) qk(sl, sacc, sodd, dma);
+    if constexpr (C::QS) {
+      f32x4* xs = reinterpret_cast<f32x4*>(lds_ring + C::kRingRows * kChunksMax);
+      const int wave = kw * C::WK + jw;
+      const int other = wave ^ HW;   // same heads, other channel half
+      if (live) {
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt) {
+          sacc[mt] += sodd[mt];
+          xs[(wave * C::MT + mt) * 64 + lane] = sacc[mt];
+        }
+      }
+      lds_barrier();
+      if (live) {
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt) {
+          sacc[mt] += xs[(other * C::MT + mt) * 64 + lane];
+          sodd[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+    if (live) {
+      smax(sacc, sodd, step, pk);
+      pv(sl, pk, [](int) {});
     }
   }
 
@@ -383,7 +468,7 @@ struct Fwd {
         else wait_vm<(C::NST > 3 ? 2 * C::OPS : 0)>();
       }
       step_sync();
-      if (it < nsteps) {
+      if (it < nsteps || C::QS) {
         const bool more = it + C::NST - 1 < nsteps;
         Dma d;
         if (more) prep(d, (J + C::NST - 1) % C::NST, it + C::NST - 1);
@@ -398,7 +483,75 @@ struct Fwd {
     }
   }
 
+  // -- software-pipelined step loop (one key-group, 4-slot ring) -------------
+  // Iteration it runs QK^T of step it + 1 and the softmax of step it, which
+  // are independent (the MFMAs of the one overlap the VALU work of the
+  // other), then P.V of step it with the DMA of step it + 3 going into the
+  // slot that step it - 1 freed. Steps up to it + 2 have been issued when
+  // iteration it starts.
+  static constexpr bool kPipe = !KVF && C::NST == 4 && C::KW == 1 && NW == 4;
+  __device__ __forceinline__ void wait_steps(int n) {   // my DMAs of all but the n newest steps
+    if constexpr (C::NI % C::WK) {
+      wait_vm_rt(n * nops);
+    } else {
+      if (n <= 0) wait_vm<0>();
+      else if (n == 1) wait_vm<C::OPS>();
+      else wait_vm<2 * C::OPS>();
+    }
+  }
+  template <int J>
+  __device__ __forceinline__ void pipe_j(int it0, f32x4 (&se)[C::MT], f32x4 (&so)[C::MT]) {
+    const int it = it0 + J;
+    if (it >= nsteps) return;   // uniform: one key-group
+    constexpr int Jn = (J + 1) % 4, Jf = (J + 3) % 4;
+    const bool nxt = it + 1 < nsteps;
+    if (nxt) wait_steps(it + 2 < nsteps ? 1 : 0);
+    step_sync();
+    uint32_t pk[2 * C::MT];
+    float sv[C::MT][4], lsum = 0.f;
+    smax_a(se, so, it, sv);
+    f32x4 ne[C::MT], no[C::MT];
+    if (nxt) {
+      qk<true>(slot(Jn), ne, no, [](int) {}, [&](int ks) {
+        if (ks < kSmaxB) smax_b(ks, sv, lsum, pk);
+      });
+#pragma unroll
+      for (int e = C::KSQ; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
+    } else {
+#pragma unroll
+      for (int e = 0; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
+    }
+    const bool more = it + 3 < nsteps;
+    Dma d;
+    if (more) prep(d, Jf, it + 3);
+    pv(slot(J), pk, [&](int o) { if (more) fire(d, o); });
+    if (nxt) {
+#pragma unroll
+      for (int mt = 0; mt < C::MT; ++mt) { se[mt] = ne[mt]; so[mt] = no[mt]; }
+    }
+  }
+  __device__ __forceinline__ void run_pipe() {
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      if (j < nsteps) issue(j, j);
+    if (nsteps <= 0) return;
+    wait_steps(min(2, nsteps - 1));
+    step_sync();
+    f32x4 se[C::MT], so[C::MT];
+    qk(slot(0), se, so, [](int) {});
+    for (int it0 = 0; it0 < nsteps; it0 += 4) {
+      pipe_j<0>(it0, se, so);
+      pipe_j<1>(it0, se, so);
+      pipe_j<2>(it0, se, so);
+      pipe_j<3>(it0, se, so);
+    }
+  }
+
   __device__ __forceinline__ void run() {
+    if constexpr (kPipe) {
+      run_pipe();
+      return;
+    }
     if constexpr (!KVF) {
 #pragma unroll
       for (int j = 0; j < C::NST - 1; ++j)
@@ -515,7 +668,7 @@ sas_fwd_kernel(const FwdParams p) {
   resolve<NW * 64, C::ROWB>(p, k, tid, lane, wave, [&] {
     const uint4* qp = reinterpret_cast<const uint4*>(p.q + ((size_t)k.t * p.H + hq) * D * 2);
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) f.qf[ks] = qp[ks * 4 + f.g];
+    for (int ks = 0; ks < C::KSQ; ++ks) f.qf[ks] = qp[((C::QS ? f.cs * C::KSQ : 0) + ks) * 4 + f.g];
   });
   const int nvalid = k.nvalid;
 
@@ -813,13 +966,12 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   while (hw > 1 && a->H % (16 * hw)) hw >>= 1;
   int nw = a->waves;
   const bool fp8 = a->kv_dtype == SAS_DT_FP8_E4M3_ROW656;
-  // 8 waves (two per SIMD, each holding half of its heads' O channels): the
-  // second wave on a SIMD overlaps the first one's softmax and LDS waits,
-  // which pays once 64 heads share the tiles (prefill: 814 vs 863 µs at 4K
-  // tokens); decode splits stay at 4 waves. The fp8 staging registers only
-  // fit 4 waves.
+  // 8 waves: two per SIMD, a pair per 16 heads splitting both the QK^T and
+  // the O channels; the second wave on a SIMD overlaps the other's LDS and
+  // softmax latencies (measured: 4K prefill 593 vs 650 µs, 32-token decode
+  // split kernel 19.3 vs 20.4 µs). The fp8 staging registers only fit 4 waves.
   if (nw == 8 && fp8) nw = 4;
-  if (nw <= 0) nw = (hw == 4 && !fp8) ? 8 : 4;
+  if (nw <= 0) nw = (hw >= 2 && !fp8) ? 8 : 4;
   if (nw != 4 && nw != 8) return sas::set_error(SAS_EINVAL, "waves must be 4 or 8");
   if (hw == 1) nw = 4;
   pl->nw = nw;

@@ -152,6 +152,16 @@ def test_head_grouping_does_not_change_result(hw):
     _check_baseline(out, lse, ref_out, ref_lse, f"C2 hw{hw}")
 
 
+@pytest.mark.parametrize("hw,waves", [(2, 4), (2, 8), (4, 4), (4, 8)])
+def test_wave_layout_does_not_change_result(hw, waves):
+    """4 or 8 waves per workgroup (with 8, each 16-head pair of waves splits
+    the QK^T channels and the O channels) only changes the work split."""
+    inp = _inputs("C2")
+    ref_out, ref_lse = _oracle(inp)
+    out, lse, _ = _run(inp, head_waves=hw, waves=waves)
+    _check_baseline(out, lse, ref_out, ref_lse, f"C2 hw{hw} waves{waves}")
+
+
 # ---------------------------------------------------------------------------
 # the reference suite's scenarios (same data as its _build_case)
 # ---------------------------------------------------------------------------
