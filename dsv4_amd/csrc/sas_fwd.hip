@@ -681,11 +681,12 @@ sas_fwd_kernel(const FwdParams p) {
   f.nsteps = (f.nrows + C::TR - 1) / C::TR;
   f.nsteps_max = per / C::TR;
 
-  // retire every load the compiler tracks (Q, tables, indices) before the
-  // DMA ring starts, so none of its own vmcnt waits lands inside the loop
-  __builtin_amdgcn_s_waitcnt(0);
+  // retire every load the compiler tracks (Q, tables, indices, sink) before
+  // the DMA ring starts, so none of its own vmcnt waits lands inside the loop
   const bool seed_sink = p.nsplit == 1 && f.kw == 0;
-  f.m_run = seed_sink ? p.sinks[hq] * kLog2e : -INFINITY;
+  const float sink = seed_sink ? p.sinks[hq] : 0.f;
+  __builtin_amdgcn_s_waitcnt(0);
+  f.m_run = seed_sink ? sink * kLog2e : -INFINITY;
   f.l_run = seed_sink ? 1.f : 0.f;
 #pragma unroll
   for (int i = 0; i < C::NTL; ++i) f.acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
