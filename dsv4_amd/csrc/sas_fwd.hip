@@ -189,8 +189,7 @@ struct Fwd {
         for (int i = 0; i < 8; ++i) {
           const uint32_t b0 = (w[i >> 1] >> ((i & 1) * 16)) & 0xffu;
           const uint32_t b1 = (w[i >> 1] >> ((i & 1) * 16 + 8)) & 0xffu;
-          o[i] = f32_to_bf16_bits(e4m3_to_f32(b0) * fsc[k]) |
-                 (f32_to_bf16_bits(e4m3_to_f32(b1) * fsc[k]) << 16);
+          o[i] = pack2<__bf16>(e4m3_to_f32(b0) * fsc[k], e4m3_to_f32(b1) * fsc[k]);
         }
         row[(2 * c) ^ sw] = make_uint4(o[0], o[1], o[2], o[3]);
         row[(2 * c + 1) ^ sw] = make_uint4(o[4], o[5], o[6], o[7]);
@@ -315,8 +314,8 @@ struct Fwd {
     } else if (e == MT * 4) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        pk[mt * 2 + 0] = to_bits<QT>(sv[mt][0]) | (to_bits<QT>(sv[mt][1]) << 16);
-        pk[mt * 2 + 1] = to_bits<QT>(sv[mt][2]) | (to_bits<QT>(sv[mt][3]) << 16);
+        pk[mt * 2 + 0] = pack2<QT>(sv[mt][0], sv[mt][1]);
+        pk[mt * 2 + 1] = pack2<QT>(sv[mt][2], sv[mt][3]);
       }
     } else {
       l_run += rows_sum(lsum);
@@ -773,7 +772,7 @@ struct Dec {
       for (int i = 0; i < 4; ++i) {
         const uint32_t b0 = (w[i >> 1] >> ((i & 1) * 16)) & 0xffu;
         const uint32_t b1 = (w[i >> 1] >> ((i & 1) * 16 + 8)) & 0xffu;
-        o[i] = f32_to_bf16_bits(e4m3_to_f32(b0) * sc) | (f32_to_bf16_bits(e4m3_to_f32(b1) * sc) << 16);
+        o[i] = pack2<__bf16>(e4m3_to_f32(b0) * sc, e4m3_to_f32(b1) * sc);
       }
       return make_uint4(o[0], o[1], o[2], o[3]);
     }
@@ -828,8 +827,7 @@ struct Dec {
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
     l_run += lsum;
-    const uint2 pfrag = make_uint2(to_bits<QT>(pv[0]) | (to_bits<QT>(pv[1]) << 16),
-                                   to_bits<QT>(pv[2]) | (to_bits<QT>(pv[3]) << 16));
+    const uint2 pfrag = make_uint2(pack2<QT>(pv[0], pv[1]), pack2<QT>(pv[2], pv[3]));
     // O^T[512 x 16] += V^T . P^T: one transposed read per 16-channel tile
     // (rows 4g + c16/4, channels mt*16 + 4*(c16&3)), 16x16x16 MFMA
     const int vr = 4 * g + (c16 >> 2);

@@ -70,23 +70,14 @@ struct FwdParams {
 // element helpers
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite inputs)
-  return u >> 16;
-}
-
-__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
-  _Float16 h = (_Float16)f;
-  return (uint32_t)__builtin_bit_cast(uint16_t, h);
-}
-
+// Two floats rounded to nearest-even 16-bit values, a in the low half
+// (one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
 template <typename QT>
-__device__ __forceinline__ uint32_t to_bits(float f);
-template <>
-__device__ __forceinline__ uint32_t to_bits<__bf16>(float f) { return f32_to_bf16_bits(f); }
-template <>
-__device__ __forceinline__ uint32_t to_bits<_Float16>(float f) { return f32_to_f16_bits(f); }
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  typedef QT v2 __attribute__((ext_vector_type(2)));
+  const v2 v = {(QT)a, (QT)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 // OCP e4m3fn byte -> float (bias 7, subnormals m * 2^-9; 0x7f/0xff NaN are
 // never produced by the cache writer, which saturates at 448).
@@ -213,8 +204,8 @@ __device__ __forceinline__ void lds_barrier() {
 
 template <typename QT>
 __device__ __forceinline__ void store_out4(const FwdParams& p, int t, int h, int c4, float4 o, float inv) {
-  const uint32_t w0 = to_bits<QT>(o.x * inv) | (to_bits<QT>(o.y * inv) << 16);
-  const uint32_t w1 = to_bits<QT>(o.z * inv) | (to_bits<QT>(o.w * inv) << 16);
+  const uint32_t w0 = pack2<QT>(o.x * inv, o.y * inv);
+  const uint32_t w1 = pack2<QT>(o.z * inv, o.w * inv);
   *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + ((size_t)t * p.H + h) * kDV + c4 * 4) =
       make_uint2(w0, w1);
 }
