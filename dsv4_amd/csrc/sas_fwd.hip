@@ -273,31 +273,43 @@ struct Fwd {
   // rescaled when the reference max moves.
   // smax_a: scaled, masked scores sv and the rescale; smax_b(e) for e in
   // [0, MT * 4 + 2): exp of score e, then the packing of P, then the sum.
+  // kChains: S still in two accumulation chains (sacc + sodd).
+  template <bool kChains = C::CH2>
   __device__ __forceinline__ void smax_a(f32x4 (&sacc)[C::MT], const f32x4 (&sodd)[C::MT], int step,
                                          float (&sv)[C::MT][4]) {
     constexpr int MT = C::MT;
     const int nk = min(C::TR, nrows - step * C::TR);
-    if constexpr (C::CH2) {
+    if constexpr (kChains) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) sacc[mt] += sodd[mt];
     }
     float mloc = -INFINITY;
+    if (nk >= C::TR) {   // a full step: no key to mask
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = mt * 16 + g * 4 + j;
-        const float x = key < nk ? sacc[mt][j] * p.scale_log2 : -INFINITY;
-        sv[mt][j] = x;
-        mloc = fmaxf(mloc, x);
-      }
+        for (int j = 0; j < 4; ++j) {
+          sv[mt][j] = sacc[mt][j] * p.scale_log2;
+          mloc = fmaxf(mloc, sv[mt][j]);
+        }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = mt * 16 + g * 4 + j;
+          const float x = key < nk ? sacc[mt][j] * p.scale_log2 : -INFINITY;
+          sv[mt][j] = x;
+          mloc = fmaxf(mloc, x);
+        }
+    }
     mloc = rows_max(mloc);
     // Lazy rescale: m_run is a reference max, moved (and O, l rescaled) only
     // when some head's max rises more than kLazyLog2 above it, so P <= 2^8.
     // out = acc / l and lse = m_run + log2 l are exact for any reference.
     if (__ballot(mloc > m_run + kLazyLog2)) {
       const float m_new = fmaxf(m_run, mloc);
-      const float alpha = exp2f(m_run - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
       m_run = m_new;
 #pragma unroll
@@ -309,7 +321,8 @@ struct Fwd {
     constexpr int MT = C::MT;
     if (e < MT * 4) {
       float& x = sv[e / 4][e % 4];
-      x = exp2f(x - m_run);
+      // v_exp_f32: results below 2^-126 flush to zero (against a row sum >= 1)
+      x = __builtin_amdgcn_exp2f(x - m_run);
       lsum = e == 0 ? x : lsum + x;
     } else if (e == MT * 4) {
 #pragma unroll
@@ -412,7 +425,7 @@ struct Fwd {
   __device__ __forceinline__ void compute(int sl, int step, DmaFn&& dma) {
     f32x4 sacc[C::MT], sodd[C::MT];
     uint32_t pk[2 * C::MT];
-    const bool live = step < nsteps;
+    const bool live = C::KW == 1 || step < nsteps;   // one key-group: every step is live
     if (live) qk(sl, sacc, sodd, dma);
     if constexpr (C::QS) {
       f32x4* xs = reinterpret_cast<f32x4*>(lds_ring + C::kRingRows * kChunksMax);
@@ -428,11 +441,14 @@ struct Fwd {
       lds_barrier();
       if (live) {
 #pragma unroll
-        for (int mt = 0; mt < C::MT; ++mt) {
-          sacc[mt] += xs[(other * C::MT + mt) * 64 + lane];
-          sodd[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+        for (int mt = 0; mt < C::MT; ++mt) sacc[mt] += xs[(other * C::MT + mt) * 64 + lane];
+        float sv[C::MT][4], lsum = 0.f;
+        smax_a<false>(sacc, sodd, step, sv);
+#pragma unroll
+        for (int e = 0; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
+        pv(sl, pk, [](int) {});
       }
+      return;
     }
     if (live) {
       smax(sacc, sodd, step, pk);
@@ -821,7 +837,7 @@ struct Dec {
     float pv[4], lsum = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      pv[j] = exp2f(sv[j] - m_run);
+      pv[j] = __builtin_amdgcn_exp2f(sv[j] - m_run);
       lsum += pv[j];
     }
     lsum += __shfl_xor(lsum, 16);
