@@ -70,7 +70,9 @@ struct Cfg {
   static constexpr int TR = kRingRows / (KW * 32) < 2 ? 16 : 32;
   static constexpr int PFK = TR == 16 ? 4 : SAS_PFK;        // K operand reads ahead
   static constexpr int PFV = TR == 16 ? 8 : SAS_PFV;        // V^T operand reads ahead
-  static constexpr bool CH2 = true;                         // two QK^T accumulation chains
+  // two QK^T accumulation chains (one suffices for the half k-range of a
+  // channel-split wave, which shares its SIMD with a second wave)
+  static constexpr bool CH2 = !QS;
   static constexpr int MT = TR / 16;                        // 16-key tiles per step
   static constexpr int NST = kRingRows / (KW * TR) > 4 ? 4 : kRingRows / (KW * TR);   // ring depth per key-group
   static constexpr int SLOT = TR * kChunksMax;              // slot stride (chunks)
@@ -434,7 +436,7 @@ struct Fwd {
       if (live) {
 #pragma unroll
         for (int mt = 0; mt < C::MT; ++mt) {
-          sacc[mt] += sodd[mt];
+          if constexpr (C::CH2) sacc[mt] += sodd[mt];
           xs[(wave * C::MT + mt) * 64 + lane] = sacc[mt];
         }
       }
