@@ -293,6 +293,10 @@ EDGE = {
     "swa_only": dict(B=3, H=64, q_lens=[1, 2, 1], kv_lens=[50, 700, 128], K=0, scenario=1),
     "fp8_small": dict(B=2, H=64, q_lens=[1, 2], kv_lens=[3000, 900], K=128, fp8=True),
     "fp16": dict(B=2, H=64, q_lens=[1, 2], kv_lens=[3000, 900], K=128, dtype=torch.float16),
+    # D = 512 through the channel-split 8-wave kernel: 32-head groups (decode)
+    # and 64-head groups (600 query rows)
+    "d512": dict(B=2, H=64, q_lens=[3, 2], kv_lens=[2500, 800], K=100, D=512),
+    "d512_prefill": dict(B=1, H=64, q_lens=[600], kv_lens=[2400], K=128, D=512),
 }
 
 
