@@ -646,22 +646,48 @@ __device__ __forceinline__ void epilogue(const FwdParams& p, const Tok& k, int t
       __syncthreads();
     }
   }
+  // The key-group-0 waves write their 16 heads x NTL * 16 channels: staged
+  // through LDS (one region per wave, its own writes then reads, in order)
+  // so every store instruction covers whole runs of a head's row instead of
+  // 16 short pieces of 16 rows. The ring is free: every wave has left the
+  // step loop (the key-group merge ends with a barrier; one key-group takes
+  // one here).
+  if constexpr (KW == 1) __syncthreads();
   if (kw == 0) {
+    const int h0 = k.hg * nhead_wg + hw * 16;   // first head of this wave
     if (!split) {
+      constexpr int kRowH = NTL * 16 + 16;      // staged row, 16-bit values (32 B pad)
+      constexpr int kCph = NTL * 16 * 2 / 16;   // 16-byte chunks per head
+      static_assert(NW * 16 * kRowH * 2 <= kLdsRows * kChunksMax * 16, "output staging fits");
+      uint16_t* sb = reinterpret_cast<uint16_t*>(lds_ring) + (size_t)jw * 16 * kRowH;
       const float inv = k.padded ? 0.f : 1.f / L;
 #pragma unroll
       for (int mt = 0; mt < NTL; ++mt)
-        store_out4<QT>(p, t, hq, (ch0 >> 2) + mt * 4 + g,
-                       make_float4(acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]), inv);
+        *reinterpret_cast<uint2*>(sb + c16 * kRowH + mt * 16 + g * 4) =
+            make_uint2(pack2<QT>(acc[mt][0] * inv, acc[mt][1] * inv), pack2<QT>(acc[mt][2] * inv, acc[mt][3] * inv));
+      uint16_t* ob = reinterpret_cast<uint16_t*>(p.out) + ((size_t)t * p.H + h0) * kDV + ch0;
+#pragma unroll
+      for (int i = 0; i < 16 * kCph / 64; ++i) {
+        const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 8;
+        *reinterpret_cast<uint4*>(ob + (size_t)h * kDV + c) = *reinterpret_cast<const uint4*>(sb + h * kRowH + c);
+      }
       if (g == 0 && cs == 0) p.lse[(size_t)t * p.H + hq] = k.padded ? 0.f : M * kLn2 + logf(L);
     } else {
-      const size_t row = ((size_t)t * p.nsplit + k.sp) * p.H + hq;
-      float* po = p.part_o + row * kDV + ch0;
+      constexpr int kRowF = NTL * 16 + 4;       // staged row, floats (16 B pad)
+      constexpr int kCph = NTL * 16 / 4;        // 16-byte chunks per head
+      static_assert(NW * 16 * kRowF * 4 <= kLdsRows * kChunksMax * 16, "partial staging fits");
+      float* sf = reinterpret_cast<float*>(lds_ring) + (size_t)jw * 16 * kRowF;
 #pragma unroll
-      for (int mt = 0; mt < NTL; ++mt)
-        *reinterpret_cast<f32x4*>(po + mt * 16 + g * 4) = acc[mt];
+      for (int mt = 0; mt < NTL; ++mt) *reinterpret_cast<f32x4*>(sf + c16 * kRowF + mt * 16 + g * 4) = acc[mt];
+      const size_t row0 = ((size_t)t * p.nsplit + k.sp) * p.H + h0;
+      float* po = p.part_o + row0 * kDV + ch0;
+#pragma unroll
+      for (int i = 0; i < 16 * kCph / 64; ++i) {
+        const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 4;
+        *reinterpret_cast<f32x4*>(po + (size_t)h * kDV + c) = *reinterpret_cast<const f32x4*>(sf + h * kRowF + c);
+      }
       if (g == 0 && cs == 0)   // l < 0 marks a padded token
-        *reinterpret_cast<float2*>(p.part_ml + row * 2) = make_float2(M, k.padded ? -1.f : L);
+        *reinterpret_cast<float2*>(p.part_ml + (row0 + c16) * 2) = make_float2(M, k.padded ? -1.f : L);
     }
   }
 }
