@@ -73,6 +73,13 @@ struct Cfg {
   // two QK^T accumulation chains (one suffices for the half k-range of a
   // channel-split wave, which shares its SIMD with a second wave)
   static constexpr bool CH2 = !QS;
+  // Paired QK^T (channel-split waves, 32-row steps): the head-waves 2h and
+  // 2h + 1 of a channel half share their K operand reads. Each of the two
+  // computes S for both their head tiles over one 16-row half of the step
+  // (two MFMAs per K fragment read, half the K reads of a wave per head),
+  // and the S pieces meet in LDS in the layout P.V reads.
+  static constexpr bool Q2 = QS && TR == 32 && HW % 2 == 0;
+  static constexpr int NQ = Q2 ? 2 : 1;                     // head tiles in a wave's QK^T
   static constexpr int MT = TR / 16;                        // 16-key tiles per step
   static constexpr int NST = kRingRows / (KW * TR) > 4 ? 4 : kRingRows / (KW * TR);   // ring depth per key-group
   static constexpr int SLOT = TR * kChunksMax;              // slot stride (chunks)
@@ -103,7 +110,7 @@ struct Fwd {
   int ring;           // chunk offset of this key-group's NST slots in lds_ring
   int nrows;           // rows this key-group owns
   int nsteps, nsteps_max;
-  uint4 qf[C::KSQ];
+  uint4 qf[C::NQ][C::KSQ];   // Q^T operand of the wave's QK^T head tiles
   float m_run, l_run;
   f32x4 acc[C::NTL];
   uint4 fbuf[KVF ? C::FOPS : 1];
@@ -223,7 +230,9 @@ struct Fwd {
     // (SG chunks) after k-step ks.
     constexpr int SG = kSwzGroup<C::CH>, KPG = SG / 4;
     const int ksw = swz<C::CH>(c16);
-    const uint4* qrow = &lds_ring[sl + c16 * C::CH];
+    // Q2: one 16-row tile (rows 16 (hw & 1) + c16, same swizzle as c16), the
+    // two head tiles of the pair as the two accumulators sacc[0..1]
+    const uint4* qrow = &lds_ring[sl + ((C::Q2 ? (hw & 1) * 16 : 0) + c16) * C::CH];
     int qo[KPG];
 #pragma unroll
     for (int j = 0; j < KPG; ++j) {
@@ -234,38 +243,41 @@ struct Fwd {
       return qrow[mt * 16 * C::CH + (ks / KPG) * SG + qo[ks % KPG]];
     };
     constexpr int kPfK = C::PFK;
-    uint4 af[kPfK][MT];
+    constexpr int RT = C::Q2 ? 1 : MT;   // K row tiles read per k-step
+    uint4 af[kPfK][RT];
 #pragma unroll
     for (int i = 0; i < kPfK; ++i)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) af[i][mt] = kfrag(i, mt);
+      for (int mt = 0; mt < RT; ++mt) af[i][mt] = kfrag(i, mt);
     // even / odd k-steps accumulate separately: 2 MT independent MFMA chains
 #pragma unroll
     for (int ks = 0; ks < C::KSQ; ++ks) {
-      uint4 a[MT];
+      uint4 a[RT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) a[mt] = af[ks % kPfK][mt];
+      for (int mt = 0; mt < RT; ++mt) a[mt] = af[ks % kPfK][mt];
       if (ks + kPfK < C::KSQ) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) af[ks % kPfK][mt] = kfrag(ks + kPfK, mt);
+        for (int mt = 0; mt < RT; ++mt) af[ks % kPfK][mt] = kfrag(ks + kPfK, mt);
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        if (C::CH2 && (ks & 1)) sodd[mt] = mfma32k<QT>(a[mt], qf[ks], sodd[mt]);
-        else sacc[mt] = mfma32k<QT>(a[mt], qf[ks], sacc[mt]);
+        const uint4 am = a[C::Q2 ? 0 : mt];
+        const uint4 bq = qf[C::Q2 ? mt : 0][ks];
+        if (C::CH2 && (ks & 1)) sodd[mt] = mfma32k<QT>(am, bq, sodd[mt]);
+        else sacc[mt] = mfma32k<QT>(am, bq, sacc[mt]);
       }
       if ((ks & 1) && ks / 2 < C::OPS) dma(ks / 2);
       if constexpr (kMid) mid(ks);
     }
 #pragma unroll
     for (int o = C::KSQ / 2; o < C::OPS; ++o) dma(o);
-    // schedule: the prefetch reads first, then per k-step MT MFMAs + MT reads
+    // schedule: the prefetch reads first, then per k-step MT MFMAs + RT reads
     // (+ a share of the other step's VALU work)
-    __builtin_amdgcn_sched_group_barrier(0x100, MT * kPfK, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, RT * kPfK, 0);
 #pragma unroll
     for (int ks = 0; ks < C::KSQ; ++ks) {
       __builtin_amdgcn_sched_group_barrier(0x008, MT, 0);
-      if (ks + kPfK < C::KSQ) __builtin_amdgcn_sched_group_barrier(0x100, MT, 0);
+      if (ks + kPfK < C::KSQ) __builtin_amdgcn_sched_group_barrier(0x100, RT, 0);
       if constexpr (kMid) __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
     }
   }
@@ -433,17 +445,23 @@ struct Fwd {
       f32x4* xs = reinterpret_cast<f32x4*>(lds_ring + C::kRingRows * kChunksMax);
       const int wave = kw * C::WK + jw;
       const int other = wave ^ HW;   // same heads, other channel half
+      // Q2 piece (head tile ht, row tile rt, channel half c) of this key-group
+      auto piece = [&](int ht, int rt, int c) { return (((kw * HW + ht) * 2 + rt) * 2 + c) * 64 + lane; };
       if (live) {
 #pragma unroll
         for (int mt = 0; mt < C::MT; ++mt) {
           if constexpr (C::CH2) sacc[mt] += sodd[mt];
-          xs[(wave * C::MT + mt) * 64 + lane] = sacc[mt];
+          if constexpr (C::Q2) xs[piece((hw & ~1) + mt, hw & 1, cs)] = sacc[mt];
+          else xs[(wave * C::MT + mt) * 64 + lane] = sacc[mt];
         }
       }
       lds_barrier();
       if (live) {
 #pragma unroll
-        for (int mt = 0; mt < C::MT; ++mt) sacc[mt] += xs[(other * C::MT + mt) * 64 + lane];
+        for (int mt = 0; mt < C::MT; ++mt) {
+          if constexpr (C::Q2) sacc[mt] = xs[piece(hw, mt, 0)] + xs[piece(hw, mt, 1)];
+          else sacc[mt] += xs[(other * C::MT + mt) * 64 + lane];
+        }
         float sv[C::MT][4], lsum = 0.f;
         smax_a<false>(sacc, sodd, step, sv);
 #pragma unroll
@@ -711,7 +729,13 @@ sas_fwd_kernel(const FwdParams p) {
   resolve<NW * 64, C::ROWB>(p, k, tid, lane, wave, [&] {
     const uint4* qp = reinterpret_cast<const uint4*>(p.q + ((size_t)k.t * p.H + hq) * D * 2);
 #pragma unroll
-    for (int ks = 0; ks < C::KSQ; ++ks) f.qf[ks] = qp[((C::QS ? f.cs * C::KSQ : 0) + ks) * 4 + f.g];
+    for (int n = 0; n < C::NQ; ++n) {
+      // head tile hw, or with Q2 the pair's tiles (hw & ~1) + n
+      const int dh = C::Q2 ? ((f.hw & ~1) + n - f.hw) * 16 : 0;
+#pragma unroll
+      for (int ks = 0; ks < C::KSQ; ++ks)
+        f.qf[n][ks] = qp[(long long)dh * (D / 8) + ((C::QS ? f.cs * C::KSQ : 0) + ks) * 4 + f.g];
+    }
   });
   const int nvalid = k.nvalid;
 
