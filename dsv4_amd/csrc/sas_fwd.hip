@@ -989,8 +989,13 @@ __global__ void __launch_bounds__(kCombineThreads)
 sas_combine_kernel(const FwdParams p) {
   constexpr int kHeads = kCombineThreads / (kDV / 4);  // 2
   const int nhb = (p.H + kHeads - 1) / kHeads;
-  const int t = blockIdx.x / nhb;
-  const int h0 = (blockIdx.x % nhb) * kHeads;
+  // token t's workgroups go to the XCD its split workgroups ran on
+  // (item_index's dealing), whose L2 still holds the partials they wrote
+  // (measured: C2 call 24.3 -> 23.7 µs)
+  const int x = (int)(blockIdx.x % kXcds), l = (int)(blockIdx.x / kXcds);
+  const int t = p.T - 1 - ((l / nhb) * kXcds + x);
+  if (t < 0) return;
+  const int h0 = (l % nhb) * kHeads;
   merge_partials<QT>(p, t, h0, min(kHeads, p.H - h0), threadIdx.x, kCombineThreads);
 }
 
@@ -1095,7 +1100,7 @@ int dispatch_hw(int hw, int nw, const FwdParams& fp, int nb, hipStream_t st) {
 
 int launch_combine(const FwdParams& fp, int out_dtype, hipStream_t st) {
   constexpr int kHeads = kCombineThreads / (kDV / 4);
-  const dim3 grid((unsigned)(fp.T * ((fp.H + kHeads - 1) / kHeads)));
+  const dim3 grid((unsigned)(((fp.T + kXcds - 1) / kXcds) * kXcds * ((fp.H + kHeads - 1) / kHeads)));
   if (out_dtype == SAS_DT_BF16)
     hipLaunchKernelGGL(sas_combine_kernel<__bf16>, grid, dim3(kCombineThreads), 0, st, fp);
   else if (out_dtype == SAS_DT_FP16)
