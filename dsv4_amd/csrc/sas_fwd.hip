@@ -726,7 +726,7 @@ sas_fwd_kernel(const FwdParams p) {
   const int hq = k.hg * (16 * HW) + f.hw * 16 + f.c16;
   // Q^T operand in registers (head hq, channels ks*32 + 8g .. +8), loaded
   // behind the block-table reads of the slot resolution
-  resolve<NW * 64, C::ROWB>(p, k, tid, lane, wave, [&] {
+  resolve<256, C::ROWB>(p, k, tid, lane, wave, [&] {
     const uint4* qp = reinterpret_cast<const uint4*>(p.q + ((size_t)k.t * p.H + hq) * D * 2);
 #pragma unroll
     for (int n = 0; n < C::NQ; ++n) {

@@ -42,6 +42,7 @@ static __shared__ __attribute__((aligned(16))) uint4 lds_ring[kLdsRows * kChunks
 static __shared__ uint64_t lds_rows[kMaxSlots];
 static __shared__ int lds_cnt[kRoundsMax][kMaxWaves];
 static __shared__ float lds_ml[kMaxWaves][2][16];
+static __shared__ int lds_tok[2];   // resolve(): the token's batch and padded flag
 
 struct FwdParams {
   const uint8_t* q;
@@ -290,7 +291,12 @@ __device__ __forceinline__ Tok item_of(const FwdParams& p, int item) {
 
 // Resolve the item's slot range to cache rows and compact the valid ones, in
 // slot order, into lds_rows[0, nvalid) as row byte addresses (ROWB bytes per
-// row), so the streaming loops only add a chunk offset. `mid` runs after the
+// row), so the streaming loops only add a chunk offset. The first NT threads
+// (waves 0 .. NT/64 - 1, the older wave of each SIMD when the workgroup has
+// 8) do the slot work; the others only run `mid` and join the compaction
+// barriers. With all 8 waves resolving, the table reads of waves 4-7 came
+// back 1-2 µs after those of waves 0-3 and the compaction waited for them
+// (4K prefill 580 -> 573 µs with 4 resolving waves). `mid` runs after the
 // block-table loads are issued (a caller can put its own loads behind them
 // there).
 template <int NT, int ROWB, typename Mid>
@@ -298,6 +304,7 @@ __device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int
   constexpr int NWV = NT / 64;
   constexpr int kRounds = (kMaxSlots + NT - 1) / NT;
   static_assert(kRounds <= kRoundsMax && NWV <= kMaxWaves, "resolve geometry");
+  const bool worker = tid < NT;   // wave-uniform
   const int t = k.t;
   const int wincap = p.win_left + 1;
   const int nslots = wincap + (p.scenario >= SAS_CFA ? p.K : 0);
@@ -305,47 +312,50 @@ __device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int
   const int s1 = min(s0 + p.slots_per_split, nslots);
   const int nr = (s1 - s0 + NT - 1) / NT;   // slot rounds of NT (<= kRounds)
 
-  // ---- round trip 1: top-k indices and batch scalars ------------------------
-  int idxv[kRounds];
-#pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    idxv[r] = -1;
-    const int j = s0 + r * NT + tid;
-    if (r < nr && p.scenario == SAS_SCFA && j < s1 && j >= wincap)
-      idxv[r] = p.cmp_idx[(size_t)t * p.K + (j - wincap)];
-  }
-  int qp0 = INT_MAX, aq0 = 0, akv0 = 0;
-  if (lane < p.B) { qp0 = p.q_prefix[lane]; aq0 = p.act_q[lane]; akv0 = p.act_kv[lane]; }
-  // token -> (batch, position): largest b with q_prefix[b] <= t (q_prefix is
-  // non-decreasing), one ballot per 64 batches
-  int b = 0, aq = 0, akv = 0, qpb = 0;
-  {
-    uint64_t m = __ballot(qp0 <= t);
-    int n = __popcll(m);
-    if (n) { b = n - 1; qpb = __shfl(qp0, n - 1); aq = __shfl(aq0, n - 1); akv = __shfl(akv0, n - 1); }
-    for (int c = 64; n == 64 && c < p.B; c += 64) {
-      const int i = c + lane;
-      int qpi = INT_MAX, aqi = 0, akvi = 0;
-      if (i < p.B) { qpi = p.q_prefix[i]; aqi = p.act_q[i]; akvi = p.act_kv[i]; }
-      m = __ballot(qpi <= t);
-      n = __popcll(m);
-      if (n) { b = c + n - 1; qpb = __shfl(qpi, n - 1); aq = __shfl(aqi, n - 1); akv = __shfl(akvi, n - 1); }
-    }
-  }
-  const int spos = t - qpb;
-  const bool padded = spos < 0 || spos >= aq;
-  const int sg = akv - aq + spos;                              // causal position
-  const int nwin = (padded || sg < 0) ? 0 : min(sg, p.win_left) + 1;
-  const int wlo = sg - nwin + 1;                               // = max(sg - win_left, 0)
-  const int thr = (padded || sg + 1 <= 0) ? 0 : (sg + 1) / p.cmp_ratio;
-
-  // ---- round trip 2: block tables -------------------------------------------
-  // Every table read is issued unconditionally at a clamped, in-range
-  // address (validity is kept apart), so the reads of all rounds are in
-  // flight together and retire with one wait.
   uint64_t rad[kRounds];
   bool val[kRounds];
-  {
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) { rad[r] = 0; val[r] = false; }
+  if (worker) {
+    // ---- round trip 1: top-k indices and batch scalars ----------------------
+    int idxv[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      idxv[r] = -1;
+      const int j = s0 + r * NT + tid;
+      if (r < nr && p.scenario == SAS_SCFA && j < s1 && j >= wincap)
+        idxv[r] = p.cmp_idx[(size_t)t * p.K + (j - wincap)];
+    }
+    int qp0 = INT_MAX, aq0 = 0, akv0 = 0;
+    if (lane < p.B) { qp0 = p.q_prefix[lane]; aq0 = p.act_q[lane]; akv0 = p.act_kv[lane]; }
+    // token -> (batch, position): largest b with q_prefix[b] <= t (q_prefix is
+    // non-decreasing), one ballot per 64 batches
+    int b = 0, aq = 0, akv = 0, qpb = 0;
+    {
+      uint64_t m = __ballot(qp0 <= t);
+      int n = __popcll(m);
+      if (n) { b = n - 1; qpb = __shfl(qp0, n - 1); aq = __shfl(aq0, n - 1); akv = __shfl(akv0, n - 1); }
+      for (int c = 64; n == 64 && c < p.B; c += 64) {
+        const int i = c + lane;
+        int qpi = INT_MAX, aqi = 0, akvi = 0;
+        if (i < p.B) { qpi = p.q_prefix[i]; aqi = p.act_q[i]; akvi = p.act_kv[i]; }
+        m = __ballot(qpi <= t);
+        n = __popcll(m);
+        if (n) { b = c + n - 1; qpb = __shfl(qpi, n - 1); aq = __shfl(aqi, n - 1); akv = __shfl(akvi, n - 1); }
+      }
+    }
+    const int spos = t - qpb;
+    const bool padded = spos < 0 || spos >= aq;
+    const int sg = akv - aq + spos;                              // causal position
+    const int nwin = (padded || sg < 0) ? 0 : min(sg, p.win_left) + 1;
+    const int wlo = sg - nwin + 1;                               // = max(sg - win_left, 0)
+    const int thr = (padded || sg + 1 <= 0) ? 0 : (sg + 1) / p.cmp_ratio;
+    if (tid == 0) { lds_tok[0] = b; lds_tok[1] = padded; }
+
+    // ---- round trip 2: block tables -----------------------------------------
+    // Every table read is issued unconditionally at a clamped, in-range
+    // address (validity is kept apart), so the reads of all rounds are in
+    // flight together and retire with one wait.
     const int32_t* obt = p.ori_bt + (size_t)b * p.ori_bt_stride;
     const int32_t* cbt = p.cmp_bt ? p.cmp_bt + (size_t)b * p.cmp_bt_stride : obt;
     int phys[kRounds], off[kRounds];
@@ -384,13 +394,15 @@ __device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int
       const int row = val[r] ? phys[r] * (ori[r] ? p.ori_bs : p.cmp_bs) + off[r] : 0;
       rad[r] = reinterpret_cast<uint64_t>(ori[r] ? p.ori_kv : p.cmp_kv) + (uint64_t)(uint32_t)row * ROWB;
     }
+  } else {
+    mid();
   }
   // ---- compaction (ballot + per-wave counts) -------------------------------
   uint64_t vmask[kRounds];
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     vmask[r] = __ballot(val[r]);
-    if (r < nr && lane == 0) lds_cnt[r][wave] = __popcll(vmask[r]);
+    if (worker && r < nr && lane == 0) lds_cnt[r][wave] = __popcll(vmask[r]);
   }
   __syncthreads();
   int nvalid = 0;
@@ -408,10 +420,10 @@ __device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int
       lds_rows[nvalid + wpre + __popcll(vmask[r] & ((1ull << lane) - 1ull))] = rad[r];
     nvalid += tot;
   }
+  k.b = lds_tok[0];
+  k.padded = lds_tok[1] != 0;
   __syncthreads();
-  k.b = b;
   k.nvalid = nvalid;
-  k.padded = padded;
 }
 
 }  // namespace sas
