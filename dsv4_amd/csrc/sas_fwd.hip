@@ -80,6 +80,12 @@ struct Cfg {
   // and the S pieces meet in LDS in the layout P.V reads.
   static constexpr bool Q2 = QS && TR == 32 && HW % 2 == 0;
   static constexpr int NQ = Q2 ? 2 : 1;                     // head tiles in a wave's QK^T
+  // 8 waves: the workgroup's query rows reach LDS by DMA (waves 4-7, which
+  // do no slot resolution), one row per head from row kQRow0 on, in the
+  // swizzled K-tile layout; every wave then reads its Q^T fragments there.
+  // The rows lie outside the slots of the first ring fill.
+  static constexpr bool QL = QS;
+  static constexpr int kQRow0 = kLdsRows - 16 * HW;
   static constexpr int MT = TR / 16;                        // 16-key tiles per step
   static constexpr int NST = kRingRows / (KW * TR) > 4 ? 4 : kRingRows / (KW * TR);   // ring depth per key-group
   static constexpr int SLOT = TR * kChunksMax;              // slot stride (chunks)
@@ -99,6 +105,9 @@ struct Cfg {
   static_assert(KW * NST * SLOT <= kRingRows * kChunksMax, "ring fits");
   static_assert(!QS || (KS % 2 == 0 && NW * 64 * MT * 4 * 4 <= (kLdsRows - kRingRows) * kChunksMax * 16),
                 "S exchange fits above the ring");
+  // the last key-group's first fill (slots 0 .. NST - 2) ends at or before kQRow0
+  static_assert(!QL || (NW == 8 && (KW - 1) * NST * TR + (NST - 1) * TR <= kQRow0),
+                "query rows clear of the first fill");
 };
 
 template <int HW, int NW, int D, typename QT, int KVF>
@@ -159,6 +168,35 @@ struct Fwd {
     prep(d, j, step);
 #pragma unroll
     for (int o = 0; o < C::OPS; ++o) fire(d, o);
+  }
+
+  // -- query rows via LDS (QL) -----------------------------------------------
+  // Waves 4-7 DMA the workgroup's 16 HW query rows (head h of the group at
+  // LDS row kQRow0 + h, chunk c at c ^ swz(h)); after the caller's wait and
+  // barrier every wave reads its Q^T fragments like K-operand fragments.
+  __device__ __forceinline__ void q_dma(const Tok& k, int wave) const {
+    constexpr int NIQ = 16 * HW * C::CH / 64;   // DMA instructions
+    static_assert(NIQ * 64 == 16 * HW * C::CH, "whole instructions");
+    const uint8_t* qb = p.q + ((size_t)k.t * p.H + k.hg * 16 * HW) * D * 2;
+    const uint32_t lb = lds_addr_of(&lds_ring[C::kQRow0 * kChunksMax]);
+    for (int i = wave - 4; i < NIQ; i += 4) {   // wave-uniform
+      const int P = i * 64 + lane, r = P / C::CH, pc = P - r * C::CH;
+      dma16(qb + (size_t)r * D * 2 + (pc ^ swz<C::CH>(r)) * 16, __builtin_amdgcn_readfirstlane(lb + i * 64 * 16));
+    }
+  }
+  __device__ __forceinline__ void q_from_lds() {
+    constexpr int SG = kSwzGroup<C::CH>;
+#pragma unroll
+    for (int n = 0; n < C::NQ; ++n) {
+      const int h = (C::Q2 ? (hw & ~1) + n : hw) * 16 + c16;   // head in the group
+      const int hsw = swz<C::CH>(h);
+      const uint4* qr = &lds_ring[C::kQRow0 * kChunksMax + h * C::CH];
+#pragma unroll
+      for (int ks = 0; ks < C::KSQ; ++ks) {
+        const int L = 4 * (cs * C::KSQ + ks) + g;
+        qf[n][ks] = qr[(L & -SG) | ((L & (SG - 1)) ^ hsw)];
+      }
+    }
   }
 
   // -- fp8 rows: global -> registers, dequantised into a slot on store -------
@@ -724,9 +762,14 @@ sas_fwd_kernel(const FwdParams p) {
   Tok k = item_of(p, item);
   Fwd<HW, NW, D, QT, KVF> f(p, lane, wave);
   const int hq = k.hg * (16 * HW) + f.hw * 16 + f.c16;
-  // Q^T operand in registers (head hq, channels ks*32 + 8g .. +8), loaded
-  // behind the block-table reads of the slot resolution
+  // Q^T operand in registers (head hq, channels ks*32 + 8g .. +8): with QL
+  // through LDS (DMA by the waves that do no slot resolution, at once), else
+  // loaded behind the block-table reads of the slot resolution
   resolve<256, C::ROWB>(p, k, tid, lane, wave, [&] {
+    if constexpr (C::QL) {
+      if (wave >= 4) f.q_dma(k, wave);
+      return;
+    }
     const uint4* qp = reinterpret_cast<const uint4*>(p.q + ((size_t)k.t * p.H + hq) * D * 2);
 #pragma unroll
     for (int n = 0; n < C::NQ; ++n) {
@@ -753,6 +796,10 @@ sas_fwd_kernel(const FwdParams p) {
   const bool seed_sink = p.nsplit == 1 && f.kw == 0;
   const float sink = seed_sink ? p.sinks[hq] : 0.f;
   __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (C::QL) {
+    __syncthreads();   // every wave's query DMA has landed
+    f.q_from_lds();    // read before the first step barrier, ahead of any write to these rows
+  }
   f.m_run = seed_sink ? sink * kLog2e : -INFINITY;
   f.l_run = seed_sink ? 1.f : 0.f;
 #pragma unroll
