@@ -737,10 +737,25 @@ __device__ __forceinline__ void epilogue(const FwdParams& p, const Tok& k, int t
       for (int mt = 0; mt < NTL; ++mt) *reinterpret_cast<f32x4*>(sf + c16 * kRowF + mt * 16 + g * 4) = acc[mt];
       const size_t row0 = ((size_t)t * p.nsplit + k.sp) * p.H + h0;
       float* po = p.part_o + row0 * kDV + ch0;
+      if (p.part_nt) {
+        // non-temporal (buffer stores: a plain store loop under the same
+        // branch would be merged with the one below, dropping the hint);
+        // the range covers this wave's 16 rows, dword 3 is gfx9's raw
+        // 32-bit buffer format
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(po, 0, 16 * kDV * 4, 0x00020000);
 #pragma unroll
-      for (int i = 0; i < 16 * kCph / 64; ++i) {
-        const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 4;
-        *reinterpret_cast<f32x4*>(po + (size_t)h * kDV + c) = *reinterpret_cast<const f32x4*>(sf + h * kRowF + c);
+        for (int i = 0; i < 16 * kCph / 64; ++i) {
+          const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 4;
+          typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+          const u32x4 v = *reinterpret_cast<const u32x4*>(sf + h * kRowF + c);
+          __builtin_amdgcn_raw_buffer_store_b128(v, rs, (h * kDV + c) * 4, 0, 2 /* nt */);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16 * kCph / 64; ++i) {
+          const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 4;
+          *reinterpret_cast<f32x4*>(po + (size_t)h * kDV + c) = *reinterpret_cast<const f32x4*>(sf + h * kRowF + c);
+        }
       }
       if (g == 0 && cs == 0)   // l < 0 marks a padded token
         *reinterpret_cast<float2*>(p.part_ml + (row0 + c16) * 2) = make_float2(M, k.padded ? -1.f : L);
@@ -1243,6 +1258,11 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   fp.nsplit = pl.nsplit; fp.slots_per_split = pl.sps; fp.nhg = pl.nhg;
   // item_index(): ceil(T / 8) tokens per XCD, nhg * nsplit workgroups each
   const int nblocks = (int)((a->T + kXcds - 1) / kXcds) * pl.nhg * pl.nsplit * kXcds;
+  // Large partials of a grid that is resident all at once stream out during
+  // the kernel instead of leaving the L2 dirty for the writeback at its end
+  // (C2 decode: 22.7 -> 22.0 µs); with a second wave of workgroups, or small
+  // partials, the L2 copy the combine reads is worth more (C4, C1 slower).
+  fp.part_nt = pl.nsplit > 1 && nblocks <= kCus && pl.ws >= (size_t(4) << 20);
   hipStream_t st = (hipStream_t)stream;
 
   if (fp8) rc = dispatch_hw<576, __bf16, 1>(pl.hw, pl.nw, fp, nblocks, st);

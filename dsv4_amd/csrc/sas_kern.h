@@ -65,6 +65,7 @@ struct FwdParams {
   int K, scenario, cmp_ratio, win_left;
   float scale_log2;
   int nsplit, slots_per_split, nhg;
+  int part_nt;   // 1: split partials go out with non-temporal stores
 };
 
 // ---------------------------------------------------------------------------
