@@ -722,10 +722,22 @@ __device__ __forceinline__ void epilogue(const FwdParams& p, const Tok& k, int t
         *reinterpret_cast<uint2*>(sb + c16 * kRowH + mt * 16 + g * 4) =
             make_uint2(pack2<QT>(acc[mt][0] * inv, acc[mt][1] * inv), pack2<QT>(acc[mt][2] * inv, acc[mt][3] * inv));
       uint16_t* ob = reinterpret_cast<uint16_t*>(p.out) + ((size_t)t * p.H + h0) * kDV + ch0;
+      if (p.out_nt) {
+        // non-temporal, by buffer stores (see the partials below)
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(ob, 0, 16 * kDV * 2, 0x00020000);
 #pragma unroll
-      for (int i = 0; i < 16 * kCph / 64; ++i) {
-        const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 8;
-        *reinterpret_cast<uint4*>(ob + (size_t)h * kDV + c) = *reinterpret_cast<const uint4*>(sb + h * kRowH + c);
+        for (int i = 0; i < 16 * kCph / 64; ++i) {
+          const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 8;
+          typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+          __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4*>(sb + h * kRowH + c), rs,
+                                                 (h * kDV + c) * 2, 0, 2 /* nt */);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16 * kCph / 64; ++i) {
+          const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 8;
+          *reinterpret_cast<uint4*>(ob + (size_t)h * kDV + c) = *reinterpret_cast<const uint4*>(sb + h * kRowH + c);
+        }
       }
       if (g == 0 && cs == 0) p.lse[(size_t)t * p.H + hq] = k.padded ? 0.f : M * kLn2 + logf(L);
     } else {
@@ -1263,6 +1275,9 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   // (C2 decode: 22.7 -> 22.0 µs); with a second wave of workgroups, or small
   // partials, the L2 copy the combine reads is worth more (C4, C1 slower).
   fp.part_nt = pl.nsplit > 1 && nblocks <= kCus && pl.ws >= (size_t(4) << 20);
+  // An output far beyond the L2s (4K prefill: 268 MB) streams out instead of
+  // evicting the cache rows the next tokens gather (C3: 586 -> 571 µs).
+  fp.out_nt = pl.nsplit == 1 && (size_t)a->T * a->H * kDV * 2 >= (size_t(16) << 20);
   hipStream_t st = (hipStream_t)stream;
 
   if (fp8) rc = dispatch_hw<576, __bf16, 1>(pl.hw, pl.nw, fp, nblocks, st);

@@ -66,6 +66,7 @@ struct FwdParams {
   float scale_log2;
   int nsplit, slots_per_split, nhg;
   int part_nt;   // 1: split partials go out with non-temporal stores
+  int out_nt;    // 1: the output (one split) goes out with non-temporal stores
 };
 
 // ---------------------------------------------------------------------------
