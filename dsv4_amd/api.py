@@ -87,7 +87,8 @@ class PreparedCall:
         a = self.args
         ca = _lib.SasCombineArgs()
         ca.part_o = a.workspace
-        ca.part_ml = a.workspace + a.T * self.num_splits * a.H * a.DV * 4
+        pb = 4 if a.q_dtype == _lib.SAS_DT_FP16 else 2   # part_o element: fp32 under fp16 out, else fp16
+        ca.part_ml = a.workspace + a.T * self.num_splits * a.H * a.DV * pb
         ca.sinks, ca.out, ca.lse = a.sinks, a.out, a.lse
         ca.T, ca.S, ca.H, ca.DV = a.T, self.num_splits, a.H, a.DV
         ca.out_dtype = a.q_dtype

@@ -650,6 +650,32 @@ constexpr int kObufStride = kDV + 4;   // floats per staged head row (bank sprea
 constexpr int kObufChunks = 16 * kObufStride / 4;   // one wave's 16 staged head rows
 static_assert(kMaxWaves / 2 * kObufChunks <= kLdsRows * kChunksMax, "epilogue staging fits");
 
+// Store 16 staged head rows (kCph 16-byte chunks each, kRowB bytes apart in
+// LDS) to global rows kDstB bytes apart; with nt, non-temporal buffer stores
+// (a plain store loop under the same branch would be merged with the other
+// one, dropping the hint; the range covers the 16 rows, dword 3 is gfx9's
+// raw 32-bit buffer format).
+template <int kCph, int kRowB, int kDstB>
+__device__ __forceinline__ void store_rows(const uint8_t* sb, uint8_t* dst, int nt, int lane) {
+  static_assert(16 * kCph % 64 == 0, "whole store instructions");
+  if (nt) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(dst, 0, 16 * kDstB, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 16 * kCph / 64; ++i) {
+      const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 16;
+      typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+      __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4*>(sb + h * kRowB + c), rs,
+                                             h * kDstB + c, 0, 2 /* nt */);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16 * kCph / 64; ++i) {
+      const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 16;
+      *reinterpret_cast<uint4*>(dst + (size_t)h * kDstB + c) = *reinterpret_cast<const uint4*>(sb + h * kRowB + c);
+    }
+  }
+}
+
 // After the step loop every wave holds (m, l, acc) of its 16 heads over its
 // key-group's rows. The KW key-groups of each head-wave are rescaled to a
 // common max and summed pairwise through LDS (a tree: half of the remaining
@@ -711,66 +737,73 @@ __device__ __forceinline__ void epilogue(const FwdParams& p, const Tok& k, int t
   if constexpr (KW == 1) __syncthreads();
   if (kw == 0) {
     const int h0 = k.hg * nhead_wg + hw * 16;   // first head of this wave
+    // Rows staged in LDS, then stored: the output in the query dtype (one
+    // split), or the split's unnormalised partial (PartT<QT>: fp16 for bf16
+    // outputs, scaled by 2^e with one e per head and 256-channel half chosen
+    // so the half's largest |value| lies in [2^14, 2^15): exact power-of-two
+    // scaling, no overflow, 8x finer than the output's rounding; fp32 for
+    // fp16 outputs, e = 0).
+    constexpr int PES = sizeof(PartT<QT>);
+    constexpr int NH = NTL / 16;              // channel halves this wave holds
+    uint8_t* sb0 = reinterpret_cast<uint8_t*>(lds_ring);
+    int ex[NH];
+    for (int hh = 0; hh < NH; ++hh) ex[hh] = 0;
     if (!split) {
-      constexpr int kRowH = NTL * 16 + 16;      // staged row, 16-bit values (32 B pad)
-      constexpr int kCph = NTL * 16 * 2 / 16;   // 16-byte chunks per head
-      static_assert(NW * 16 * kRowH * 2 <= kLdsRows * kChunksMax * 16, "output staging fits");
-      uint16_t* sb = reinterpret_cast<uint16_t*>(lds_ring) + (size_t)jw * 16 * kRowH;
+      constexpr int kRowB = NTL * 16 * 2 + 32;   // staged row bytes (32 B pad)
+      constexpr int kCph = NTL * 16 * 2 / 16;    // 16-byte chunks per head
+      static_assert(NW * 16 * kRowB <= kLdsRows * kChunksMax * 16, "output staging fits");
+      uint8_t* sb = sb0 + (size_t)jw * 16 * kRowB;
       const float inv = k.padded ? 0.f : 1.f / L;
 #pragma unroll
       for (int mt = 0; mt < NTL; ++mt)
-        *reinterpret_cast<uint2*>(sb + c16 * kRowH + mt * 16 + g * 4) =
+        *reinterpret_cast<uint2*>(sb + c16 * kRowB + (mt * 16 + g * 4) * 2) =
             make_uint2(pack2<QT>(acc[mt][0] * inv, acc[mt][1] * inv), pack2<QT>(acc[mt][2] * inv, acc[mt][3] * inv));
-      uint16_t* ob = reinterpret_cast<uint16_t*>(p.out) + ((size_t)t * p.H + h0) * kDV + ch0;
-      if (p.out_nt) {
-        // non-temporal, by buffer stores (see the partials below)
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(ob, 0, 16 * kDV * 2, 0x00020000);
-#pragma unroll
-        for (int i = 0; i < 16 * kCph / 64; ++i) {
-          const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 8;
-          typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-          __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4*>(sb + h * kRowH + c), rs,
-                                                 (h * kDV + c) * 2, 0, 2 /* nt */);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16 * kCph / 64; ++i) {
-          const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 8;
-          *reinterpret_cast<uint4*>(ob + (size_t)h * kDV + c) = *reinterpret_cast<const uint4*>(sb + h * kRowH + c);
-        }
-      }
+      uint8_t* ob = p.out + (((size_t)t * p.H + h0) * kDV + ch0) * 2;
+      store_rows<kCph, kRowB, kDV * 2>(sb, ob, p.out_nt, lane);
       if (g == 0 && cs == 0) p.lse[(size_t)t * p.H + hq] = k.padded ? 0.f : M * kLn2 + logf(L);
     } else {
-      constexpr int kRowF = NTL * 16 + 4;       // staged row, floats (16 B pad)
-      constexpr int kCph = NTL * 16 / 4;        // 16-byte chunks per head
-      static_assert(NW * 16 * kRowF * 4 <= kLdsRows * kChunksMax * 16, "partial staging fits");
-      float* sf = reinterpret_cast<float*>(lds_ring) + (size_t)jw * 16 * kRowF;
+      constexpr int kRowB = NTL * 16 * PES + (PES == 2 ? 32 : 16);
+      constexpr int kCph = NTL * 16 * PES / 16;
+      static_assert(NW * 16 * kRowB <= kLdsRows * kChunksMax * 16, "partial staging fits");
+      uint8_t* sb = sb0 + (size_t)jw * 16 * kRowB;
+      if constexpr (PES == 2) {
 #pragma unroll
-      for (int mt = 0; mt < NTL; ++mt) *reinterpret_cast<f32x4*>(sf + c16 * kRowF + mt * 16 + g * 4) = acc[mt];
-      const size_t row0 = ((size_t)t * p.nsplit + k.sp) * p.H + h0;
-      float* po = p.part_o + row0 * kDV + ch0;
-      if (p.part_nt) {
-        // non-temporal (buffer stores: a plain store loop under the same
-        // branch would be merged with the one below, dropping the hint);
-        // the range covers this wave's 16 rows, dword 3 is gfx9's raw
-        // 32-bit buffer format
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(po, 0, 16 * kDV * 4, 0x00020000);
+        for (int hh = 0; hh < NH; ++hh) {
+          float a = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16 * kCph / 64; ++i) {
-          const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 4;
-          typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-          const u32x4 v = *reinterpret_cast<const u32x4*>(sf + h * kRowF + c);
-          __builtin_amdgcn_raw_buffer_store_b128(v, rs, (h * kDV + c) * 4, 0, 2 /* nt */);
+          for (int mt = hh * 16; mt < hh * 16 + 16; ++mt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a = fmaxf(a, fabsf(acc[mt][j]));
+          a = rows_max(a);   // over the head's four lane groups
+          int e2 = 0;
+          if (a > 0.f && a <= 3.0e38f) { (void)frexpf(a, &e2); e2 = 15 - e2; }   // a < 2^(15 - e2)
+          ex[hh] = e2;
+        }
+#pragma unroll
+        for (int mt = 0; mt < NTL; ++mt) {
+          const int e2 = ex[mt / 16];
+          *reinterpret_cast<uint2*>(sb + c16 * kRowB + (mt * 16 + g * 4) * 2) =
+              make_uint2(pack2<_Float16>(ldexpf(acc[mt][0], e2), ldexpf(acc[mt][1], e2)),
+                         pack2<_Float16>(ldexpf(acc[mt][2], e2), ldexpf(acc[mt][3], e2)));
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 16 * kCph / 64; ++i) {
-          const int q = i * 64 + lane, h = q / kCph, c = (q - h * kCph) * 4;
-          *reinterpret_cast<f32x4*>(po + (size_t)h * kDV + c) = *reinterpret_cast<const f32x4*>(sf + h * kRowF + c);
+        for (int mt = 0; mt < NTL; ++mt)
+          *reinterpret_cast<f32x4*>(sb + c16 * kRowB + (mt * 16 + g * 4) * 4) = acc[mt];
+      }
+      const size_t row0 = ((size_t)t * p.nsplit + k.sp) * p.H + h0;
+      uint8_t* ob = p.part_o + (row0 * kDV + ch0) * PES;
+      store_rows<kCph, kRowB, kDV * PES>(sb, ob, p.part_nt, lane);
+      if (g == 0) {
+        // (m, l, e_lo, e_hi); l < 0 marks a padded token
+        float* pm = p.part_ml + (row0 + c16) * 4;
+        if constexpr (NH == 2) {
+          *reinterpret_cast<float4*>(pm) = make_float4(M, k.padded ? -1.f : L, (float)ex[0], (float)ex[1]);
+        } else {
+          if (cs == 0) *reinterpret_cast<float2*>(pm) = make_float2(M, k.padded ? -1.f : L);
+          pm[2 + cs] = (float)ex[0];
         }
       }
-      if (g == 0 && cs == 0)   // l < 0 marks a padded token
-        *reinterpret_cast<float2*>(p.part_ml + (row0 + c16) * 2) = make_float2(M, k.padded ? -1.f : L);
     }
   }
 }
@@ -1077,6 +1110,9 @@ sas_combine_kernel(const FwdParams p) {
 // host side
 // ---------------------------------------------------------------------------
 
+// bytes per split-partial O element: fp16 (scaled) for bf16 outputs, fp32 for fp16 outputs
+int part_bytes(int q_dtype) { return q_dtype == SAS_DT_FP16 ? 4 : 2; }
+
 struct Plan {
   int hw, nw, nhg, nslots, nsplit, sps;
   size_t ws;
@@ -1142,7 +1178,7 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   ns = (pl->nslots + sps - 1) / sps;  // drop empty trailing splits
   pl->nsplit = std::max(ns, 1);
   pl->sps = sps;
-  pl->ws = pl->nsplit > 1 ? (size_t)a->T * pl->nsplit * a->H * (kDV + 2) * sizeof(float) : 0;
+  pl->ws = pl->nsplit > 1 ? (size_t)a->T * pl->nsplit * a->H * (kDV * part_bytes(a->q_dtype) + 4 * sizeof(float)) : 0;
   return SAS_OK;
 }
 
@@ -1193,7 +1229,7 @@ int combine_impl(const SasCombineArgs* a, hipStream_t st) {
     return sas::set_error(SAS_EINVAL, "combine: bad dims (S must be 1..64, DV 512)");
   if (a->T == 0) return SAS_OK;
   FwdParams fp{};
-  fp.part_o = const_cast<float*>(a->part_o);
+  fp.part_o = (uint8_t*)const_cast<void*>(a->part_o);
   fp.part_ml = const_cast<float*>(a->part_ml);
   fp.sinks = a->sinks;
   fp.out = (uint8_t*)a->out;
@@ -1255,8 +1291,8 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   fp.out = (uint8_t*)a->out;
   fp.lse = a->lse;
   if (pl.nsplit > 1) {
-    fp.part_o = (float*)a->workspace;
-    fp.part_ml = (float*)a->workspace + (size_t)a->T * pl.nsplit * a->H * kDV;
+    fp.part_o = (uint8_t*)a->workspace;
+    fp.part_ml = (float*)((uint8_t*)a->workspace + (size_t)a->T * pl.nsplit * a->H * kDV * part_bytes(a->q_dtype));
   }
   fp.T = (int)a->T; fp.B = (int)a->B; fp.H = (int)a->H;
   fp.ori_bs = (int)a->ori_block_size; fp.ori_bt_stride = (int)a->ori_bt_stride;

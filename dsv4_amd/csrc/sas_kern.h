@@ -57,8 +57,8 @@ struct FwdParams {
   const float* sinks;
   uint8_t* out;
   float* lse;
-  float* part_o;
-  float* part_ml;
+  uint8_t* part_o;    // [T, S, H, 512] PartT: unnormalised O x 2^e per 256-channel half
+  float* part_ml;     // [T, S, H, 4]: running max (log2 units), running sum, e of each half
   int T, B, H;
   int ori_bs, ori_bt_stride, ori_nblocks;
   int cmp_bs, cmp_bt_stride, cmp_nblocks;
@@ -213,31 +213,43 @@ __device__ __forceinline__ void store_out4(const FwdParams& p, int t, int h, int
       make_uint2(w0, w1);
 }
 
-// Merge the nsplit fp32 partials of (token t, heads [h0, h0 + nh)) with the
-// sink into out / lse: M = max(sink, m_i), L = 2^(sink-M) + sum_i l_i
-// 2^(m_i-M), out = sum_i 2^(m_i-M) O_i / L, lse = (M ln 2) + ln L (a running
-// merge over i, kB splits' loads in flight together). A negative l marks a
-// padded token (out = 0, lse = 0).
+// Split-partial O element type: fp16 under bf16 outputs (scaled by a power
+// of two per 256-channel half, 8x finer than the output's rounding), fp32
+// under fp16 outputs (fp16 would round as coarsely as the output does).
+template <typename QT> struct PartSel { using T = _Float16; };
+template <> struct PartSel<_Float16> { using T = float; };
+template <typename QT> using PartT = typename PartSel<QT>::T;
+
+// Merge the nsplit partials of (token t, heads [h0, h0 + nh)) with the sink
+// into out / lse: M = max(sink, m_i), L = 2^(sink-M) + sum_i l_i 2^(m_i-M),
+// out = sum_i 2^(m_i-M) O_i / L, lse = (M ln 2) + ln L (a running merge over
+// i, kB splits' loads in flight together). Partial O_i is stored as fp16
+// values O_i 2^e_i (PartT: fp16, or fp32 with e_i = 0) with one exponent e_i
+// per 256-channel half, so it is recovered exactly as ldexp(value, -e_i). A negative l marks a padded token
+// (out = 0, lse = 0).
 template <typename QT>
 __device__ __forceinline__ void merge_partials(const FwdParams& p, int t, int h0, int nh, int tid,
                                                int nthreads) {
   constexpr int kB = 4;
   const int S = p.nsplit;
-  const float* po = p.part_o + (size_t)t * S * p.H * kDV;
-  const float* pm = p.part_ml + (size_t)t * S * p.H * 2;
+  using PT = PartT<QT>;
+  typedef PT v4 __attribute__((ext_vector_type(4)));
+  const v4* po = reinterpret_cast<const v4*>(p.part_o) + (size_t)t * S * p.H * (kDV / 4);
+  const float* pm = p.part_ml + (size_t)t * S * p.H * 4;
   for (int e = tid; e < nh * (kDV / 4); e += nthreads) {
     const int h = h0 + e / (kDV / 4), c4 = e % (kDV / 4);
+    const int half = c4 >= kDV / 8;
     float M = p.sinks[h] * kLog2e, L = 1.f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     bool pad = false;
     for (int s0 = 0; s0 < S; s0 += kB) {
-      float2 ml[kB];
-      float4 v[kB];
+      float4 ml[kB];
+      v4 v[kB];
 #pragma unroll
       for (int j = 0; j < kB; ++j) {
         const size_t row = (size_t)min(s0 + j, S - 1) * p.H + h;
-        ml[j] = *reinterpret_cast<const float2*>(pm + row * 2);
-        v[j] = *reinterpret_cast<const float4*>(po + row * kDV + c4 * 4);
+        ml[j] = *reinterpret_cast<const float4*>(pm + row * 4);
+        v[j] = po[row * (kDV / 4) + c4];
       }
 #pragma unroll
       for (int j = 0; j < kB; ++j) {
@@ -249,8 +261,11 @@ __device__ __forceinline__ void merge_partials(const FwdParams& p, int t, int h0
           M = ml[j].x;
         }
         const float w = ml[j].x == -INFINITY ? 0.f : exp2f(ml[j].x - M);
+        const int ne = -(int)(half ? ml[j].w : ml[j].z);
+        const v4 x = v[j];
         L += w * ml[j].y;
-        o.x += w * v[j].x; o.y += w * v[j].y; o.z += w * v[j].z; o.w += w * v[j].w;
+        o.x += ldexpf(w * (float)x[0], ne); o.y += ldexpf(w * (float)x[1], ne);
+        o.z += ldexpf(w * (float)x[2], ne); o.w += ldexpf(w * (float)x[3], ne);
       }
     }
     store_out4<QT>(p, t, h, c4, o, pad ? 0.f : 1.f / L);

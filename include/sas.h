@@ -121,8 +121,9 @@ typedef struct SasFwdArgs {
 } SasFwdArgs;
 
 /* SasFwdArgs.flags: with more than one split, stop after the split kernel and
-   leave the fp32 partials in the workspace (part_o at offset 0, part_ml after
-   T*S*H*DV floats, S = the planned split count); the caller then runs
+   leave the partials in the workspace (part_o at offset 0, part_ml after
+   T*S*H*DV partial elements, S = the planned split count; layout as in
+   SasCombineArgs); the caller then runs
    sas_combine_v1 itself, e.g. to time or overlap the two kernels apart. */
 #define SAS_FWD_NO_COMBINE 1
 
@@ -145,11 +146,16 @@ int sas_fwd_v1(const SasFwdArgs* a, void* stream);
  * flash-decode fields stay zero, metadata.py:323-325): for each (token, head)
  * M = max(sink, m_i), L = e^(sink-M) + sum_i l_i e^(m_i-M),
  * out = sum_i e^(m_i-M) O_i / L, lse = M + ln L.
- * part_o [T, S, H, DV] fp32 (unnormalised), part_ml [T, S, H, 2] fp32
- * (running max in log2 units, running sum).
+ * part_o [T, S, H, DV]: the unnormalised O_i scaled by 2^e, with one integer
+ * e per (token, split, head) and 256-channel half (O_i = value * 2^-e,
+ * exactly); elements are fp16 when out_dtype is bf16 (e puts each half's
+ * largest |value| in [2^14, 2^15)) and fp32 when out_dtype is fp16 (e = 0 as
+ * written by sas_fwd_v1); part_ml [T, S, H, 4] fp32: (running max in log2 units, running
+ * sum, e of channels 0-255, e of channels 256-511). A negative running sum
+ * marks a padded token (out = 0, lse = 0).
  */
 typedef struct SasCombineArgs {
-  const float* part_o;
+  const void* part_o;
   const float* part_ml;
   const float* sinks;
   void* out;

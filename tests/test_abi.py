@@ -56,13 +56,13 @@ def test_plan_valid():
     rc, ns, ws = _plan(_valid_args())
     assert rc == _lib.SAS_OK
     assert ns >= 1
-    assert ws == (0 if ns == 1 else 4 * ns * 64 * (512 + 2) * 4)
+    assert ws == (0 if ns == 1 else 4 * ns * 64 * (512 * 2 + 4 * 4))   # fp16 part_o + (m, l, e, e)
 
 
 def test_plan_explicit_splits_and_workspace():
     rc, ns, ws = _plan(_valid_args(num_splits=3))
     assert rc == _lib.SAS_OK and ns == 3
-    assert ws == 4 * 3 * 64 * 514 * 4
+    assert ws == 4 * 3 * 64 * (512 * 2 + 16)
 
 
 @pytest.mark.parametrize("field,value,needle", [

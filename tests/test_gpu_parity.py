@@ -345,31 +345,45 @@ def test_bsnd_layout_with_padding():
     assert torch.count_nonzero(lse[1, 1:].cpu()) == 0
 
 
-def test_combine_entry_point_closed_form():
-    """sas_combine_v1 against the closed-form LSE merge on random partials."""
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_combine_entry_point_closed_form(out_dtype):
+    """sas_combine_v1 against the closed-form LSE merge on random partials:
+    values (fp16 under bf16 outputs, fp32 under fp16 outputs) with one
+    power-of-two exponent per (token, split, head, 256-channel half),
+    including exponents far outside fp16's range."""
     T, S, H, DV = 3, 5, 32, 512
     g = torch.Generator().manual_seed(1)
-    po = torch.randn(T, S, H, DV, generator=g)
+    vals = torch.randn(T, S, H, DV, generator=g)
+    vals = vals.to(torch.float16) if out_dtype == torch.bfloat16 else vals
+    lo = -20 if out_dtype == torch.bfloat16 else 0   # fp16 outputs: keep |out| below 65504
+    ex = torch.randint(lo, 40, (T, S, H, 2), generator=g).float()
+    ex[0, 1, 3, 0] = 120.0                      # O around 2^-120
+    ex[2, 0, 5, 1] = -100.0                     # O around 2^100 (l large too)
     m2 = torch.randn(T, S, H, generator=g) * 3
     l = torch.rand(T, S, H, generator=g) * 10 + 0.1
+    l[2, 0, 5] = 2.0 ** 100
     m2[1, 2] = -math.inf          # an empty split
     l[1, 2] = 0.0
     sinks = torch.randn(H, generator=g)
-    ml = torch.stack([m2, l], dim=-1).contiguous()
-    out = torch.empty(T, H, DV, dtype=torch.bfloat16, device="cuda")
+    ml = torch.stack([m2, l, ex[..., 0], ex[..., 1]], dim=-1).contiguous()
+    out = torch.empty(T, H, DV, dtype=out_dtype, device="cuda")
     lse = torch.empty(T, H, dtype=torch.float32, device="cuda")
-    dpo, dml, ds = po.cuda(), ml.cuda(), sinks.cuda()
+    dpo, dml, ds = vals.cuda(), ml.cuda(), sinks.cuda()
     a = _lib.SasCombineArgs(part_o=dpo.data_ptr(), part_ml=dml.data_ptr(), sinks=ds.data_ptr(),
                             out=out.data_ptr(), lse=lse.data_ptr(), T=T, S=S, H=H, DV=DV,
-                            out_dtype=_lib.SAS_DT_BF16)
+                            out_dtype=_lib.SAS_DT_BF16 if out_dtype == torch.bfloat16 else _lib.SAS_DT_FP16)
     st = torch.cuda.current_stream().cuda_stream
     _lib.check(_lib.lib().sas_combine_v1(C.byref(a), C.c_void_p(st)), "combine")
     torch.cuda.synchronize()
     ln2 = math.log(2.0)
-    m_nat = m2 * ln2                                    # partial maxima, natural log
-    M = torch.maximum(sinks.view(1, H), m_nat.amax(dim=1))
-    w = torch.exp(m_nat - M.unsqueeze(1))               # [T, S, H]
-    L = torch.exp(sinks.view(1, H) - M) + (w * l).sum(dim=1)
+    scale = torch.cat([ex[..., :1].expand(T, S, H, DV // 2), ex[..., 1:].expand(T, S, H, DV // 2)], dim=-1)
+    po = vals.double() * torch.pow(2.0, -scale.double())   # the partial O the values encode
+    m_nat = (m2 * ln2).double()                             # partial maxima, natural log
+    sk = sinks.double().view(1, H)
+    M = torch.maximum(sk, m_nat.amax(dim=1))
+    w = torch.exp(m_nat - M.unsqueeze(1))                   # [T, S, H]
+    L = torch.exp(sk - M) + (w * l.double()).sum(dim=1)
     ref = (w.unsqueeze(-1) * po).sum(dim=1) / L.unsqueeze(-1)
-    torch.testing.assert_close(out.cpu().float(), ref.to(torch.bfloat16).float(), atol=1e-2, rtol=1e-2)
-    torch.testing.assert_close(lse.cpu(), M + torch.log(L), atol=1e-5, rtol=1e-5)
+    tol = 1e-2 if out_dtype == torch.bfloat16 else 2e-3
+    torch.testing.assert_close(out.cpu().float(), ref.to(out_dtype).float(), atol=tol, rtol=tol)
+    torch.testing.assert_close(lse.cpu().double(), M + torch.log(L), atol=1e-5, rtol=1e-5)
