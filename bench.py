@@ -194,6 +194,40 @@ def measure_traffic(kv_bytes_hint=None):
 # ---------------------------------------------------------------------------
 
 
+CW_ROWS = 32768        # rows per cache-write call: a 32K-token prefill chunk
+CW_ROTATIONS = 8       # distinct inputs and cache blocks: 474 MB touched, beyond the MALL
+
+
+def bench_cache_write():
+    """sas_cache_write_v1 quantising CW_ROWS bf16 rows (D = 576) into 656-byte
+    fp8 rows through a shuffled block table (bs 64). Algorithmic HBM bytes per
+    row: 1152 read + 656 written + 8 of (batch, position)."""
+    from dsv4_amd.cache import prepare_kv_cache_write
+    g = torch.Generator(device="cuda").manual_seed(11)
+    bs, B = 64, 16
+    per_b = CW_ROWS // B
+    nblk = per_b // bs
+    nb = CW_ROTATIONS * B * nblk
+    cache = torch.zeros(nb, bs, 1, 656, dtype=torch.uint8, device="cuda")
+    perm = torch.randperm(nb, device="cuda", generator=g).to(torch.int32)
+    sid = torch.arange(B, device="cuda", dtype=torch.int32).repeat_interleave(per_b)
+    pos = torch.arange(per_b, device="cuda", dtype=torch.int32).repeat(B)
+    calls = []
+    for r in range(CW_ROTATIONS):
+        kv = torch.randn(CW_ROWS, 576, device="cuda", generator=g).to(torch.bfloat16)
+        table = perm[r * B * nblk:(r + 1) * B * nblk].reshape(B, nblk).contiguous()
+        calls.append(prepare_kv_cache_write(kv, cache, table, sid, pos))
+    torch.cuda.synchronize()
+    ms, _ = time_launches(lambda i, st: calls[i].launch(st), len(calls), 240, 12)
+    us = ms * 1e3 / 240
+    byts = CW_ROWS * (1152 + 656 + 8)
+    gbs = byts / (us * 1e-6) / 1e9
+    return dict(workload=f"fp8 cache write: {CW_ROWS} bf16 rows (D 576) -> 656-byte rows, "
+                         f"shuffled block table bs {bs}", us_per_call=round(us, 3),
+                bytes=byts, gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
+                _log=f"cache write: {us:.2f} us/call, {gbs:.0f} GB/s ({byts} B)")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -204,6 +238,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-traffic", action="store_true")
+    ap.add_argument("--no-cache-write", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -285,6 +320,12 @@ def main():
                        mfma_frac=round(tfl / BF16_PEAK_TFLOPS, 4), splits=pcall.num_splits)
         log(f"C3 prefill: {pus:.1f} us/call, {tfl:.1f} TFLOP/s ({flops:.4e} useful FLOP)")
 
+    # ---------------- paged-KV cache writer (fp8 rows) ------------------------
+    cwrite = None
+    if not args.no_cache_write:
+        cwrite = bench_cache_write()
+        log(cwrite.pop("_log"))
+
     # ---------------- CPU baseline (oracle on host cores) --------------------
     cpu = None
     if not args.no_cpu:
@@ -335,6 +376,7 @@ def main():
                      "kernel": f"{SPLIT_KERNEL} (C2 split-KV forward, {ns} splits)",
                      "traffic_detail": traffic if traffic else traffic_note},
         "prefill": prefill,
+        "cache_write": cwrite,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

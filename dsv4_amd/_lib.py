@@ -20,7 +20,7 @@ SAS_META_SIZE = 1024
 SAS_FWD_NO_COMBINE = 1
 
 EXPORTED = ("sas_metadata_v1", "sas_fwd_plan", "sas_fwd_v1", "sas_combine_v1",
-            "sas_last_error", "sas_version")
+            "sas_cache_write_v1", "sas_last_error", "sas_version")
 
 _i32p = C.POINTER(C.c_int32)
 
@@ -73,6 +73,16 @@ class SasCombineArgs(C.Structure):
     ]
 
 
+class SasCacheWriteArgs(C.Structure):
+    _fields_ = [
+        ("kv", C.c_void_p), ("seq_ids", C.c_void_p), ("positions", C.c_void_p),
+        ("block_table", C.c_void_p), ("cache", C.c_void_p),
+        ("N", C.c_int64), ("B", C.c_int64), ("D", C.c_int64), ("kv_stride", C.c_int64),
+        ("bt_stride", C.c_int64), ("block_size", C.c_int64), ("num_blocks", C.c_int64),
+        ("kv_dtype", C.c_int32), ("cache_dtype", C.c_int32),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -96,6 +106,8 @@ def lib() -> C.CDLL:
                 L.sas_fwd_v1.restype = C.c_int
                 L.sas_combine_v1.argtypes = [C.POINTER(SasCombineArgs), C.c_void_p]
                 L.sas_combine_v1.restype = C.c_int
+                L.sas_cache_write_v1.argtypes = [C.POINTER(SasCacheWriteArgs), C.c_void_p]
+                L.sas_cache_write_v1.restype = C.c_int
                 L.sas_last_error.argtypes = []
                 L.sas_last_error.restype = C.c_char_p
                 L.sas_version.argtypes = []

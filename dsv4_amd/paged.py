@@ -277,8 +277,11 @@ def fill_normal(shape, dtype, gen: torch.Generator, device) -> torch.Tensor:
 def quantize_kv_fp8(kv: torch.Tensor) -> torch.Tensor:
     """Pack ``[..., 576]`` KV rows (latent 512 + rope 64) into 656-byte rows.
 
-    Per 128-channel group: ``scale = amax / 448`` (1 for an all-zero group),
-    ``byte = e4m3fn(x / scale)`` rounded to nearest even.
+    Per 128-channel group: ``scale = amax / 448`` is stored and
+    ``byte = e4m3fn(clamp(x * inv, -448, 448))`` with ``inv = 448 / amax``
+    (both 1 for an all-zero group), rounded to nearest even: one division per
+    group, a multiply per value (the device writer computes the same fp32
+    products, so both write the same bytes).
     """
     if kv.shape[-1] != FP8_LATENT + FP8_ROPE:
         raise ValueError(f"fp8 rows need 576 channels, got {kv.shape[-1]}")
@@ -286,8 +289,13 @@ def quantize_kv_fp8(kv: torch.Tensor) -> torch.Tensor:
     x = kv.reshape(-1, FP8_LATENT + FP8_ROPE).float()
     lat = x[:, :FP8_LATENT].reshape(-1, FP8_NGROUPS, FP8_GROUP)
     amax = lat.abs().amax(dim=-1)
-    scale = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
-    q8 = (lat / scale.unsqueeze(-1)).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    nz = amax > 0
+    scale = torch.where(nz, amax / E4M3_MAX, torch.ones_like(amax))
+    # a tensor / tensor division (correctly rounded, as on the device); torch
+    # evaluates `scalar / tensor` as reciprocal(tensor) * scalar
+    inv = torch.where(nz, torch.full_like(amax, E4M3_MAX).div(torch.where(nz, amax, torch.ones_like(amax))),
+                      torch.ones_like(amax))
+    q8 = (lat * inv.unsqueeze(-1)).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
     rows = torch.empty((x.shape[0], FP8_ROW_BYTES), dtype=torch.uint8, device=kv.device)
     rows[:, :FP8_LATENT] = q8.reshape(-1, FP8_LATENT).view(torch.uint8)
     rows[:, FP8_SCALE_OFF:FP8_ROPE_OFF] = scale.contiguous().view(torch.uint8).reshape(-1, 16)

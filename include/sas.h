@@ -166,6 +166,35 @@ typedef struct SasCombineArgs {
 
 int sas_combine_v1(const SasCombineArgs* a, void* stream);
 
+/*
+ * Paged-KV cache writer (no counterpart in the reference, whose tests build
+ * paged caches on the host in the layout of golden.py:315-408; this is the
+ * device-side producer of that layout). Input row r (of N) goes to the cache
+ * row of batch seq_ids[r] at logical position positions[r]: physical block
+ * block_table[b * bt_stride + pos / block_size], offset pos % block_size.
+ * Rows with a negative position, a batch outside [0, B), a position past the
+ * table, or a table entry outside [0, num_blocks) (-1 = unused) are skipped.
+ * cache_dtype == kv_dtype: the D channels are copied. cache_dtype ==
+ * SAS_DT_FP8_E4M3_ROW656 (bf16 kv, D = 576): per 128 latent channels
+ * scale = amax / 448 is stored and byte = e4m3fn(clamp(x * inv, -448, 448))
+ * with inv = 448 / amax (both 1 for an all-zero group), rounded to nearest
+ * even; rope channels copied as bf16. Rows written by one
+ * call must be distinct (two rows to one cache row race).
+ */
+typedef struct SasCacheWriteArgs {
+  const void* kv;                /* [N, kv_stride] kv_dtype, 16-byte aligned rows */
+  const int32_t* seq_ids;        /* [N] batch of each row */
+  const int32_t* positions;      /* [N] logical position in that batch's cache */
+  const int32_t* block_table;    /* [B, bt_stride] */
+  void* cache;                   /* [num_blocks, block_size, 1, row] */
+  int64_t N, B, D, kv_stride;    /* kv_stride in elements */
+  int64_t bt_stride, block_size, num_blocks;
+  int32_t kv_dtype;              /* SAS_DT_BF16 or SAS_DT_FP16 */
+  int32_t cache_dtype;           /* kv_dtype, or SAS_DT_FP8_E4M3_ROW656 */
+} SasCacheWriteArgs;
+
+int sas_cache_write_v1(const SasCacheWriteArgs* a, void* stream);
+
 /* Thread-local message of the last failed call on this thread ("" if none). */
 const char* sas_last_error(void);
 
