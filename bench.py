@@ -44,6 +44,7 @@ METRIC = "decode µs/call + HBM GB/s (B32,H64,k512+w128); prefill TFLOP/s at 4K"
 SPLIT_KERNEL = "sas_fwd_kernel"
 COMBINE_KERNEL = "sas_combine_kernel"
 CAL_KERNEL = "neg_kernel"      # torch.neg on fp32: reads and writes numel*4 bytes
+CW_KERNEL = "sas_cache_fp8_kernel"
 CAL_NUMEL = 32 << 20           # 128 MiB each way
 PMC_ROTATIONS = 4              # 94 MB of gathered rows: beyond the 32 MB of L2
 
@@ -131,12 +132,18 @@ def pmc_pass():
             c.launch_split()
             c.launch_combine()
     torch.cuda.synchronize()
+    del calls, inp
+    cw = _cache_write_calls()
+    for _ in range(2):
+        for c in cw:
+            c.launch()
+    torch.cuda.synchronize()
     print("[pmc-pass] done", flush=True)
 
 
 def _read_counter(outdir, counter):
     """{kernel substring: [per-dispatch values]} for the counter."""
-    vals = {SPLIT_KERNEL: [], COMBINE_KERNEL: [], CAL_KERNEL: []}
+    vals = {SPLIT_KERNEL: [], COMBINE_KERNEL: [], CAL_KERNEL: [], CW_KERNEL: []}
     files = glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True)
     for f in files:
         with open(f, newline="") as fh:
@@ -184,10 +191,12 @@ def measure_traffic(kv_bytes_hint=None):
         # skip the first pass over the rotations (cold TLB / first touch)
         split = v[SPLIT_KERNEL][PMC_ROTATIONS:] or v[SPLIT_KERNEL]
         comb = v[COMBINE_KERNEL][PMC_ROTATIONS:] or v[COMBINE_KERNEL]
+        cw = v[CW_KERNEL][CW_ROTATIONS:] or v[CW_KERNEL]
         out[counter] = dict(
             cal_factor=round(cal, 4),
             split_bytes=sum(split) / len(split) * 1024.0 / cal,
-            combine_bytes=(sum(comb) / len(comb) * 1024.0 / cal) if comb else None)
+            combine_bytes=(sum(comb) / len(comb) * 1024.0 / cal) if comb else None,
+            cache_write_bytes=(sum(cw) / len(cw) * 1024.0 / cal) if cw else None)
     return out, None
 
 
@@ -198,10 +207,10 @@ CW_ROWS = 32768        # rows per cache-write call: a 32K-token prefill chunk
 CW_ROTATIONS = 8       # distinct inputs and cache blocks: 474 MB touched, beyond the MALL
 
 
-def bench_cache_write():
-    """sas_cache_write_v1 quantising CW_ROWS bf16 rows (D = 576) into 656-byte
-    fp8 rows through a shuffled block table (bs 64). Algorithmic HBM bytes per
-    row: 1152 read + 656 written + 8 of (batch, position)."""
+def _cache_write_calls():
+    """CW_ROTATIONS prepared cache writes of CW_ROWS bf16 rows (D = 576, 16
+    sequences) into 656-byte fp8 rows through shuffled block tables (bs 64),
+    each rotation with its own input rows and cache blocks."""
     from dsv4_amd.cache import prepare_kv_cache_write
     g = torch.Generator(device="cuda").manual_seed(11)
     bs, B = 64, 16
@@ -218,13 +227,24 @@ def bench_cache_write():
         table = perm[r * B * nblk:(r + 1) * B * nblk].reshape(B, nblk).contiguous()
         calls.append(prepare_kv_cache_write(kv, cache, table, sid, pos))
     torch.cuda.synchronize()
+    return calls
+
+
+def bench_cache_write(traffic=None):
+    """sas_cache_write_v1 over _cache_write_calls(). Algorithmic HBM bytes per
+    row: 1152 read + 656 written + 8 of (batch, position)."""
+    bs = 64
+    calls = _cache_write_calls()
     ms, _ = time_launches(lambda i, st: calls[i].launch(st), len(calls), 240, 12)
     us = ms * 1e3 / 240
     byts = CW_ROWS * (1152 + 656 + 8)
     gbs = byts / (us * 1e-6) / 1e9
+    tr = None
+    if traffic and traffic["FETCH_SIZE"].get("cache_write_bytes") and traffic["WRITE_SIZE"].get("cache_write_bytes"):
+        tr = round(traffic["FETCH_SIZE"]["cache_write_bytes"] + traffic["WRITE_SIZE"]["cache_write_bytes"])
     return dict(workload=f"fp8 cache write: {CW_ROWS} bf16 rows (D 576) -> 656-byte rows, "
-                         f"shuffled block table bs {bs}", us_per_call=round(us, 3),
-                bytes=byts, gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
+                         f"shuffled block table bs {bs}", kernel=CW_KERNEL, us_per_call=round(us, 3),
+                bytes=byts, gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4), traffic=tr,
                 _log=f"cache write: {us:.2f} us/call, {gbs:.0f} GB/s ({byts} B)")
 
 
@@ -323,7 +343,7 @@ def main():
     # ---------------- paged-KV cache writer (fp8 rows) ------------------------
     cwrite = None
     if not args.no_cache_write:
-        cwrite = bench_cache_write()
+        cwrite = bench_cache_write(traffic)
         log(cwrite.pop("_log"))
 
     # ---------------- CPU baseline (oracle on host cores) --------------------
