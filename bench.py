@@ -322,6 +322,17 @@ def main():
         sparse_attn_sharedkv(inp.q, **kw)
     torch.cuda.synchronize()
     api_us = (time.perf_counter() - t0) / 20 * 1e6
+    # the same with cu_seqlens_q / seqused_kv already on the device
+    kwd = dict(kw, cu_seqlens_q=inp.cu_seqlens_q.cuda(), seqused_kv=inp.seqused_kv.cuda())
+    for _ in range(3):
+        sparse_attn_sharedkv(inp.q, **kwd)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        sparse_attn_sharedkv(inp.q, **kwd)
+    torch.cuda.synchronize()
+    api_dev_us = (time.perf_counter() - t0) / 20 * 1e6
+    log(f"API call: {api_us:.1f} us (host seqlens), {api_dev_us:.1f} us (device seqlens)")
 
     # ---------------- prefill, config 3 --------------------------------------
     prefill = None
@@ -390,6 +401,7 @@ def main():
         "combine_kernel_us": round(us_comb, 3),
         "num_splits": ns,
         "api_us_per_call": round(api_us, 1),
+        "api_us_per_call_device_seqlens": round(api_dev_us, 1),
         "gathered_kv_bytes": kv_bytes,
         "roofline": {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": tr,

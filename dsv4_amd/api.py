@@ -51,6 +51,7 @@ class PreparedCall:
         self.layout_q = layout_q
         self.B = B
         self.S_max = S_max
+        self._prep_stream = torch.cuda.current_stream(out.device)
         ns = C.c_int32(0)
         ws = C.c_size_t(0)
         _lib.check(_lib.lib().sas_fwd_plan(C.byref(args), C.byref(ns), C.byref(ws)),
@@ -65,6 +66,12 @@ class PreparedCall:
 
     def _stream(self, stream):
         st = stream if stream is not None else torch.cuda.current_stream(self.out.device)
+        if st != self._prep_stream:
+            # the device-side offsets and copies were enqueued on the stream
+            # that was current when the call was prepared
+            ev = torch.cuda.Event()
+            ev.record(self._prep_stream)
+            st.wait_event(ev)
         return C.c_void_p(st.cuda_stream)
 
     def launch(self, stream: Optional[torch.cuda.Stream] = None) -> None:
@@ -101,6 +108,12 @@ class PreparedCall:
         ca = self.combine_args()
         _lib.check(_lib.lib().sas_combine_v1(C.byref(ca), self._stream(stream)),
                    "sparse_attn_sharedkv combine")
+
+    def metadata(self) -> torch.Tensor:
+        """The reference's int32[1024] scheduler metadata for this call: the
+        tensor passed in, else synthesised with the bit-exact scheduler
+        (metadata.py:258-1086). The kernels do not need it."""
+        return self._metadata_fn()
 
     def result(self, return_softmax_lse: bool):
         out, lse = self.out, self.lse
@@ -155,27 +168,34 @@ def prepare_sparse_attn_sharedkv(
         _lib.SAS_CFA if cmp_sparse_indices is None else _lib.SAS_SCFA)
 
     # ---- flat [total_tokens, N1, D] view + per-batch token offsets ----------
+    # q_prefix / act_q (int32 [B]) reach the kernel as device arrays. With a
+    # device cu_seqlens_q they are computed on the device (no host sync); host
+    # values are copied through pinned memory without blocking.
+    dev_cu = None
     if layout_q == "TND":
         assert cu_seqlens_q is not None, "cu_seqlens_q is required for TND"
-        cu = cu_seqlens_q.to(torch.int32).cpu()
-        B = cu.numel() - 1
-        seq_lens = (cu[1:] - cu[:-1]).tolist()
-        S_max = max(seq_lens) if seq_lens else 0
+        B = cu_seqlens_q.numel() - 1
+        S_max = None   # not needed for TND outputs
         T1, N1, D = q.shape
         q_flat = q
-        q_prefix = cu[:-1]
-        act_q = torch.tensor(seq_lens, dtype=torch.int32)
+        if cu_seqlens_q.is_cuda:
+            dev_cu = cu_seqlens_q.to(device=dev, dtype=torch.int32).contiguous()
+            q_prefix = act_q = None
+        else:
+            cu = cu_seqlens_q.to(torch.int32)
+            q_prefix = cu[:-1]
+            act_q = cu[1:] - cu[:-1]
         idx_flat = cmp_sparse_indices if scenario == _lib.SAS_SCFA else None
     else:
         B, S_max, N1, D = q.shape
         T1 = B * S_max
         q_flat = q.reshape(T1, N1, D)
         q_prefix = torch.arange(B, dtype=torch.int32) * S_max
-        seq_lens = [S_max] * B
         if cu_seqlens_q is not None:
             cu = cu_seqlens_q.to(torch.int32).cpu()
-            seq_lens = (cu[1:] - cu[:-1]).tolist()
-        act_q = torch.tensor(seq_lens, dtype=torch.int32)
+            act_q = cu[1:] - cu[:-1]
+        else:
+            act_q = torch.full((B,), S_max, dtype=torch.int32)
         idx_flat = None
         if scenario == _lib.SAS_SCFA:
             ci = cmp_sparse_indices
@@ -214,13 +234,28 @@ def prepare_sparse_attn_sharedkv(
     if scenario >= _lib.SAS_CFA and cmp_ratio_eff < 1:
         raise ValueError("cmp_ratio must be >= 1")
 
-    # ---- metadata (api.py:335-366): synthesised when absent, validated ------
-    if metadata is None:
+    # ---- metadata (api.py:335-366) -------------------------------------------
+    # A given tensor is validated. The kernel covers every (token, head group,
+    # split) by construction and does not consume it, so an absent one is not
+    # synthesised on the call path (about 25 us of host time per call);
+    # PreparedCall.metadata() builds it with the bit-exact scheduler on demand.
+    if metadata is not None:
+        assert metadata.numel() == SAS_META_SIZE, (
+            f"metadata must have {SAS_META_SIZE} int32 entries (got {metadata.numel()})")
+
+    def _metadata():
+        if metadata is not None:
+            return metadata
+        kv_max = int(seqused_kv.max().item()) if seqused_kv.numel() else 0
+        if layout_q == "TND":
+            cu_h = cu_seqlens_q.to(torch.int32).cpu()
+            sq = int((cu_h[1:] - cu_h[:-1]).max().item()) if B else 0
+        else:
+            sq = int(S_max)
         meta_kwargs = dict(
             num_heads_q=N1, num_heads_kv=N2, head_dim=D,
             cu_seqlens_q=cu_seqlens_q if layout_q == "TND" else None,
-            seqused_kv=seqused_kv, batch_size=int(B), max_seqlen_q=int(S_max),
-            max_seqlen_kv=int(seqused_kv.max().item()) if seqused_kv.numel() else 0,
+            seqused_kv=seqused_kv, batch_size=int(B), max_seqlen_q=sq, max_seqlen_kv=kv_max,
             ori_mask_mode=ori_mask_mode, ori_win_left=ori_win_left, ori_win_right=ori_win_right,
             layout_q=layout_q, layout_kv=layout_kv, has_ori_kv=True,
             has_cmp_kv=cmp_kv is not None, aic_core_num=core_num)
@@ -229,9 +264,7 @@ def prepare_sparse_attn_sharedkv(
             meta_kwargs["cmp_mask_mode"] = cmp_mask_mode
         if scenario == _lib.SAS_SCFA:
             meta_kwargs["cmp_topk"] = K
-        metadata = sparse_attn_sharedkv_metadata(**meta_kwargs)
-    assert metadata.numel() == SAS_META_SIZE, (
-        f"metadata must have {SAS_META_SIZE} int32 entries (got {metadata.numel()})")
+        return sparse_attn_sharedkv_metadata(**meta_kwargs)
 
     # ---- device operands ------------------------------------------------------
     keep = []
@@ -250,11 +283,24 @@ def prepare_sparse_attn_sharedkv(
     ckv = d(cmp_kv) if scenario >= _lib.SAS_CFA else None
     cbt = d(cmp_block_table, torch.int32) if scenario >= _lib.SAS_CFA else None
     cidx = d(idx_flat, torch.int32) if scenario == _lib.SAS_SCFA else None
-    host = torch.cat([q_prefix.to(torch.int32), act_q,
-                      seqused_kv.to(device="cpu", dtype=torch.int32).reshape(-1)])
     if seqused_kv.numel() != B:
         raise ValueError(f"seqused_kv has {seqused_kv.numel()} entries, batch is {B}")
-    hd = d(host)
+    if dev_cu is not None:
+        qp_d = dev_cu[:-1]
+        aq_d = dev_cu[1:] - dev_cu[:-1]
+        keep.extend([dev_cu, aq_d])
+    else:
+        # one pinned staging buffer, copied without blocking the host
+        hb = torch.cat([q_prefix.to(torch.int32), act_q.to(torch.int32)]).pin_memory()
+        hd = hb.to(device=dev, non_blocking=True)
+        keep.extend([hb, hd])
+        qp_d, aq_d = hd[:B], hd[B:]
+    if seqused_kv.is_cuda:
+        akv_d = d(seqused_kv.reshape(-1), torch.int32)
+    else:
+        kb = seqused_kv.to(torch.int32).reshape(-1).contiguous().pin_memory()
+        akv_d = kb.to(device=dev, non_blocking=True)
+        keep.extend([kb, akv_d])
     snk = d(sinks, torch.float32)
     if snk.numel() != N1:
         raise ValueError(f"sinks must have {N1} entries (got {snk.numel()})")
@@ -266,9 +312,7 @@ def prepare_sparse_attn_sharedkv(
     a.cmp_kv = ckv.data_ptr() if ckv is not None else None
     a.cmp_block_table = cbt.data_ptr() if cbt is not None else None
     a.cmp_indices = cidx.data_ptr() if cidx is not None else None
-    a.q_prefix = hd.data_ptr()
-    a.act_q = hd.data_ptr() + 4 * B
-    a.act_kv = hd.data_ptr() + 8 * B
+    a.q_prefix, a.act_q, a.act_kv = qp_d.data_ptr(), aq_d.data_ptr(), akv_d.data_ptr()
     a.sinks, a.out, a.lse = snk.data_ptr(), out.data_ptr(), lse.data_ptr()
     a.T, a.B, a.H, a.D, a.DV = T1, B, N1, D, 512
     a.ori_block_size, a.ori_bt_stride, a.ori_num_blocks = okv.shape[1], obt.shape[1], okv.shape[0]
@@ -284,7 +328,9 @@ def prepare_sparse_attn_sharedkv(
     a.num_splits = int(num_splits)
     a.head_waves = int(head_waves)
     a.waves = int(waves)
-    return PreparedCall(a, keep, out, lse, layout_q, B, S_max)
+    call = PreparedCall(a, keep, out, lse, layout_q, B, S_max)
+    call._metadata_fn = _metadata
+    return call
 
 
 def sparse_attn_sharedkv(

@@ -245,6 +245,50 @@ def test_api_return_type():
     torch.testing.assert_close(out.cpu(), one.cpu())
 
 
+def test_api_host_and_device_offsets_agree():
+    """cu_seqlens_q / seqused_kv given on the host (pinned non-blocking
+    copies) or on the device (offsets derived there, no host sync) give the
+    same bits; the C4 ragged batch exercises non-trivial q offsets."""
+    inp = cases.make_inputs(cases.CONFIGS["C4"], device="cpu")
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    kw.update(cu_seqlens_q=inp.cu_seqlens_q.cuda(), seqused_kv=inp.seqused_kv.cuda())
+    dev_out, dev_lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+    kw.update(cu_seqlens_q=inp.cu_seqlens_q.cpu(), seqused_kv=inp.seqused_kv.cpu())
+    host_out, host_lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(dev_out.cpu(), host_out.cpu()) and torch.equal(dev_lse.cpu(), host_lse.cpu())
+    ref_out, ref_lse = _oracle(inp)
+    torch.testing.assert_close(dev_out.cpu().float(), ref_out.float(), atol=OUT_TOL, rtol=OUT_TOL)
+    torch.testing.assert_close(dev_lse.cpu(), ref_lse, atol=LSE_ATOL, rtol=0)
+
+
+def test_prepared_call_on_another_stream_and_metadata():
+    """A prepared call launched on a stream other than the one it was
+    prepared on (its device-side offsets are ordered first) gives the
+    one-shot result; metadata() is the scheduler's bit-exact output."""
+    from dsv4_amd.api import prepare_sparse_attn_sharedkv
+    from dsv4_amd.metadata import sparse_attn_sharedkv_metadata
+    inp = cases.make_inputs(cases.CONFIGS["C2"], device="cpu")
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    kw.update(cu_seqlens_q=inp.cu_seqlens_q.cuda(), seqused_kv=inp.seqused_kv.cuda())
+    ref = sparse_attn_sharedkv(d.q, **kw)
+    call = prepare_sparse_attn_sharedkv(d.q, **kw)
+    side = torch.cuda.Stream()
+    call.launch(side)
+    side.synchronize()
+    torch.cuda.synchronize()
+    assert torch.equal(call.out.cpu(), ref.cpu())
+    meta = sparse_attn_sharedkv_metadata(
+        num_heads_q=64, num_heads_kv=1, head_dim=576, cu_seqlens_q=inp.cu_seqlens_q,
+        seqused_kv=inp.seqused_kv, batch_size=len(inp.q_lens), max_seqlen_q=1,
+        max_seqlen_kv=int(inp.seqused_kv.max()), ori_mask_mode=4, ori_win_left=127, ori_win_right=0,
+        layout_q="TND", layout_kv="PA_ND", has_ori_kv=True, has_cmp_kv=True, aic_core_num=24,
+        cmp_ratio=4, cmp_mask_mode=3, cmp_topk=512)
+    assert torch.equal(call.metadata().cpu(), meta.cpu())
+
+
 # ---------------------------------------------------------------------------
 # edge cases
 # ---------------------------------------------------------------------------
