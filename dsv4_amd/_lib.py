@@ -20,7 +20,7 @@ SAS_META_SIZE = 1024
 SAS_FWD_NO_COMBINE = 1
 
 EXPORTED = ("sas_metadata_v1", "sas_fwd_plan", "sas_fwd_v1", "sas_combine_v1",
-            "sas_cache_write_v1", "sas_last_error", "sas_version")
+            "sas_cache_write_v1", "sas_bwd_v1", "sas_last_error", "sas_version")
 
 _i32p = C.POINTER(C.c_int32)
 
@@ -73,6 +73,13 @@ class SasCombineArgs(C.Structure):
     ]
 
 
+class SasBwdArgs(C.Structure):
+    _fields_ = [
+        ("fwd", SasFwdArgs), ("dout", C.c_void_p), ("dq", C.c_void_p),
+        ("d_ori_kv", C.c_void_p), ("d_cmp_kv", C.c_void_p), ("d_sinks", C.c_void_p),
+    ]
+
+
 class SasCacheWriteArgs(C.Structure):
     _fields_ = [
         ("kv", C.c_void_p), ("seq_ids", C.c_void_p), ("positions", C.c_void_p),
@@ -106,6 +113,8 @@ def lib() -> C.CDLL:
                 L.sas_fwd_v1.restype = C.c_int
                 L.sas_combine_v1.argtypes = [C.POINTER(SasCombineArgs), C.c_void_p]
                 L.sas_combine_v1.restype = C.c_int
+                L.sas_bwd_v1.argtypes = [C.POINTER(SasBwdArgs), C.c_void_p]
+                L.sas_bwd_v1.restype = C.c_int
                 L.sas_cache_write_v1.argtypes = [C.POINTER(SasCacheWriteArgs), C.c_void_p]
                 L.sas_cache_write_v1.restype = C.c_int
                 L.sas_last_error.argtypes = []

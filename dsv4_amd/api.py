@@ -375,3 +375,50 @@ def sparse_attn_sharedkv(
         core_num=core_num, topk_cmp=topk_cmp)
     call.launch()
     return call.result(return_softmax_lse)
+
+
+def sparse_attn_sharedkv_backward(
+    dout: torch.Tensor,
+    q: torch.Tensor,
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    **kwargs,
+) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor], torch.Tensor]:
+    """Gradients of :func:`sparse_attn_sharedkv` (the reference has no
+    backward; its LSE output is documented as this pass's input, api.py:32-35).
+
+    ``dout``, ``out`` (``[..., 512]``) and ``lse`` are in the forward's layout;
+    ``kwargs`` are the forward's keyword arguments (same caches, tables,
+    indices, seqlens, sinks, scale, scenario). Caches must be in q's dtype.
+    Returns ``(dq, d_ori_kv, d_cmp_kv, d_sinks)``: ``dq`` in q's dtype and
+    layout; the cache gradients fp32 in the caches' shapes (zero for rows no
+    token attends; ``d_cmp_kv`` is None without ``cmp_kv``); ``d_sinks`` fp32
+    ``[H]``. Key sets are the forward's: window rows and the valid top-k (or
+    dense compressed) rows; V is the first 512 channels of each row.
+    """
+    kwargs.pop("return_softmax_lse", None)
+    call = prepare_sparse_attn_sharedkv(q, **kwargs)
+    a = call.args
+    if a.kv_dtype != a.q_dtype:
+        raise ValueError("the backward needs caches in the query dtype (fp8 rows are not differentiated)")
+    T1, H = int(a.T), int(a.H)
+    dev = q.device
+    dout_f = dout.reshape(T1, H, 512)
+    out_f = out.reshape(T1, H, 512)
+    lse_f = lse.reshape(T1, H)
+    for name, t_, dt in (("dout", dout_f, q.dtype), ("out", out_f, q.dtype), ("lse", lse_f, torch.float32)):
+        if t_.dtype != dt or t_.device != dev:
+            raise ValueError(f"{name} must be a {dt} tensor on {dev}")
+    dout_f, out_f, lse_f = dout_f.contiguous(), out_f.contiguous(), lse_f.contiguous()
+    ori_kv = kwargs["ori_kv"]
+    cmp_kv = kwargs.get("cmp_kv")
+    dq = torch.empty((T1, H, int(a.D)), dtype=torch.float32, device=dev)
+    d_ori = torch.zeros(ori_kv.shape, dtype=torch.float32, device=dev)
+    d_cmp = torch.zeros(cmp_kv.shape, dtype=torch.float32, device=dev) if cmp_kv is not None else None
+    d_sinks = torch.zeros(H, dtype=torch.float32, device=dev)
+    a.out, a.lse = out_f.data_ptr(), lse_f.data_ptr()
+    ba = _lib.SasBwdArgs(fwd=a, dout=dout_f.data_ptr(), dq=dq.data_ptr(), d_ori_kv=d_ori.data_ptr(),
+                         d_cmp_kv=d_cmp.data_ptr() if d_cmp is not None else None,
+                         d_sinks=d_sinks.data_ptr())
+    _lib.check(_lib.lib().sas_bwd_v1(C.byref(ba), call._stream(None)), "sparse_attn_sharedkv_backward")
+    return dq.to(q.dtype).reshape(q.shape), d_ori, d_cmp, d_sinks

@@ -1,0 +1,268 @@
+// sparse_attn_sharedkv backward for MI355X (gfx950): dQ, dKV (the shared
+// K = V cache rows) and d(sink) from the forward's output and LSE.
+//
+// No counterpart in the reference, which documents its LSE output as the
+// input of a FlashAttention-v2 style backward (api.py:32-35, 176-184). For a
+// query token t and head h over the forward's key set J (window rows and the
+// valid top-k rows, resolved by the forward's own slot resolution) and the
+// sink:
+//   P_j = exp(scale q.k_j - lse),  P_sink = exp(sink - lse)
+//   dP_j = dO . v_j (v_j = the first 512 channels of k_j),  Delta = dO . O
+//   dS_j = P_j (dP_j - Delta)
+//   dq = scale sum_j dS_j k_j
+//   dkv_j += scale dS_j q  +  [P_j dO, 0]   (summed over heads and tokens)
+//   dsink += -P_sink Delta                   (the sink's value row is zero)
+//
+// One workgroup (4 waves) per (token, 16-head group). Thread (h, part) keeps
+// q, dO of head h for channel part `part` (D / 16 channels) in registers and
+// accumulates that part of dq. Rows stream through LDS in chunks of 16: each
+// thread's partial q.k and dO.v sums are reduce-scattered over the head's 16
+// lanes so lane `part` ends with row `part`'s score, computes P and dS, and
+// shares them through LDS; then every thread adds dS k to its dq part and
+// owns up to three channels of the chunk's dkv rows (a sum over the 16
+// heads, added to the fp32 gradient cache rows with atomics). VALU only:
+// a first, exact version; the forward's MFMA layouts are the way to speed
+// it up.
+
+#include "sas_kern.h"
+
+namespace sas {
+namespace {
+
+constexpr int kBwdRows = 16;   // rows per chunk (= lanes per head)
+
+struct BwdParams {
+  FwdParams f;
+  const uint8_t* out;   // [T, H, 512] q dtype
+  const uint8_t* dout;  // [T, H, 512] q dtype
+  float* dq;            // [T, H, D] fp32
+  float* d_ori;         // [ori rows, D] fp32, accumulated
+  float* d_cmp;         // [cmp rows, D] fp32, accumulated (null for SWA)
+  float* d_sinks;       // [H] fp32, accumulated
+};
+
+template <typename QT>
+__device__ __forceinline__ float to_f(uint16_t v) {
+  return (float)__builtin_bit_cast(QT, v);
+}
+
+// Butterfly reduce-scatter over the 16 lanes of a head: lane `part` returns
+// the lane-sum of v[part].
+__device__ __forceinline__ float reduce_scatter16(float (&v)[kBwdRows], int part) {
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) {
+    const bool up = part & o;
+#pragma unroll
+    for (int i = 0; i < o; ++i) {
+      const float send = up ? v[i] : v[i + o];
+      const float keep = up ? v[i + o] : v[i];
+      v[i] = keep + __shfl_xor(send, o);
+    }
+  }
+  return v[0];
+}
+
+__device__ __forceinline__ float sum16(float x) {
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+template <int D, typename QT>
+__global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
+  constexpr int CP = D / 16;                   // channels per part
+  constexpr int CH = D / 8;                    // 16-byte chunks per row
+  constexpr int KS = D * 2 + 16;               // LDS row stride (bytes)
+  __shared__ __attribute__((aligned(16))) uint8_t lds_k[kBwdRows * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_q[16 * D];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_do[16 * kDV];
+  __shared__ float lds_pd[kBwdRows][16][2];    // (P, scale dS) per row and head
+
+  const FwdParams& p = bp.f;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int item = item_index(p);
+  if (item < 0) return;
+  Tok k = item_of(p, item);
+  resolve<256, D * 2>(p, k, tid, lane, wave, [] {});
+  const int h = tid >> 4, part = tid & 15;
+  const int hq = k.hg * 16 + h;
+  const int t = k.t;
+  float* dqp = bp.dq + ((size_t)t * p.H + hq) * D + part * CP;
+  if (k.padded) {
+#pragma unroll
+    for (int i = 0; i < CP; ++i) dqp[i] = 0.f;
+    return;
+  }
+
+  // this thread's q / dO / O channels, Delta, and the tiles for the dkv phase
+  const uint16_t* qg = reinterpret_cast<const uint16_t*>(p.q) + ((size_t)t * p.H + hq) * D + part * CP;
+  const uint16_t* dog = reinterpret_cast<const uint16_t*>(bp.dout) + ((size_t)t * p.H + hq) * kDV;
+  const uint16_t* og = reinterpret_cast<const uint16_t*>(bp.out) + ((size_t)t * p.H + hq) * kDV;
+  float qr[CP], dr[CP], dq[CP];
+  float dpart = 0.f;
+#pragma unroll
+  for (int i = 0; i < CP; ++i) {
+    const int c = part * CP + i;
+    qr[i] = to_f<QT>(qg[i]);
+    dr[i] = c < kDV ? to_f<QT>(dog[c]) : 0.f;
+    if (c < kDV) dpart += dr[i] * to_f<QT>(og[c]);
+    dq[i] = 0.f;
+  }
+  const float delta = sum16(dpart);
+  const float lse2 = p.lse[(size_t)t * p.H + hq] * kLog2e;
+  if (part == 0) {
+    const float psink = __builtin_amdgcn_exp2f(p.sinks[hq] * kLog2e - lse2);
+    atomicAdd(bp.d_sinks + hq, -psink * delta);
+  }
+  {
+    const uint4* qs = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.q) +
+                                                     ((size_t)t * p.H + k.hg * 16) * D);
+    const uint4* ds = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(bp.dout) +
+                                                     ((size_t)t * p.H + k.hg * 16) * kDV);
+    for (int i = tid; i < 16 * D / 8; i += 256) reinterpret_cast<uint4*>(lds_q)[i] = qs[i];
+    for (int i = tid; i < 16 * kDV / 8; i += 256) reinterpret_cast<uint4*>(lds_do)[i] = ds[i];
+  }
+  const float scale = p.scale_log2 / kLog2e;
+  const uint64_t ori_lo = reinterpret_cast<uint64_t>(p.ori_kv);
+  const uint64_t ori_n = (uint64_t)p.ori_nblocks * p.ori_bs * (D * 2);
+  const uint64_t cmp_lo = reinterpret_cast<uint64_t>(p.cmp_kv);
+
+  for (int c0 = 0; c0 < k.nvalid; c0 += kBwdRows) {
+    const int nr = min(kBwdRows, k.nvalid - c0);
+    for (int i = tid; i < kBwdRows * CH; i += 256) {
+      const int r = i / CH, c = i - r * CH;
+      const uint64_t a = lds_rows[c0 + min(r, nr - 1)];
+      *reinterpret_cast<uint4*>(lds_k + r * KS + c * 16) = *reinterpret_cast<const uint4*>(a + c * 16);
+    }
+    __syncthreads();
+    float sv[kBwdRows], dv[kBwdRows];
+#pragma unroll
+    for (int r = 0; r < kBwdRows; ++r) {
+      const uint16_t* kr = reinterpret_cast<const uint16_t*>(lds_k + r * KS) + part * CP;
+      float s = 0.f, d = 0.f;
+#pragma unroll
+      for (int i = 0; i < CP; ++i) {
+        const float kv = to_f<QT>(kr[i]);
+        s += qr[i] * kv;
+        d += dr[i] * kv;   // dr is zero past channel 512
+      }
+      sv[r] = s;
+      dv[r] = d;
+    }
+    const float s_row = reduce_scatter16(sv, part);    // row `part`
+    const float dp_row = reduce_scatter16(dv, part);
+    float pr = 0.f, dsr = 0.f;
+    if (part < nr) {
+      pr = __builtin_amdgcn_exp2f(s_row * p.scale_log2 - lse2);
+      dsr = pr * (dp_row - delta) * scale;
+    }
+    lds_pd[part][h][0] = pr;
+    lds_pd[part][h][1] = dsr;
+    __syncthreads();
+    // dq part += sum_r scale dS_r k_r
+    for (int r = 0; r < nr; ++r) {
+      const float w = lds_pd[r][h][1];
+      const uint16_t* kr = reinterpret_cast<const uint16_t*>(lds_k + r * KS) + part * CP;
+#pragma unroll
+      for (int i = 0; i < CP; ++i) dq[i] += w * to_f<QT>(kr[i]);
+    }
+    // dkv rows of the chunk: channel c = tid + 256 m, summed over the heads
+    for (int r = 0; r < nr; ++r) {
+      const uint64_t a = lds_rows[c0 + r];
+      float* g = a - ori_lo < ori_n ? bp.d_ori + (a - ori_lo) / (D * 2) * D
+                                    : bp.d_cmp + (a - cmp_lo) / (D * 2) * D;
+#pragma unroll
+      for (int m = 0; m < (D + 255) / 256; ++m) {
+        const int c = tid + 256 * m;
+        if (c >= D) break;
+        float acc = 0.f;
+#pragma unroll
+        for (int hh = 0; hh < 16; ++hh) {
+          acc += lds_pd[r][hh][1] * to_f<QT>(lds_q[hh * D + c]);
+          if (c < kDV) acc += lds_pd[r][hh][0] * to_f<QT>(lds_do[hh * kDV + c]);
+        }
+        atomicAdd(g + c, acc);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < CP; ++i) dqp[i] = dq[i];
+}
+
+template <int D, typename QT>
+int launch_bwd(const BwdParams& bp, int nblocks, hipStream_t st) {
+  hipLaunchKernelGGL((sas_bwd_kernel<D, QT>), dim3(nblocks), dim3(256), 0, st, bp);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(SAS_ELAUNCH, "sas_bwd launch: %s", hipGetErrorString(e));
+  return SAS_OK;
+}
+
+}  // namespace
+}  // namespace sas
+
+extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
+  using namespace sas;
+  clear_error();
+  if (!ba) return set_error(SAS_EINVAL, "bwd: null args");
+  const SasFwdArgs* a = &ba->fwd;
+  if (a->T < 0 || a->B < 1 || a->H < 1 || a->H % 16) return set_error(SAS_EINVAL, "bwd: bad T/B/H (H a multiple of 16)");
+  if (a->D != 512 && a->D != 576) return set_error(SAS_EINVAL, "bwd: D must be 512 or 576");
+  if (a->DV != kDV) return set_error(SAS_EINVAL, "bwd: DV must be 512");
+  if (a->scenario < SAS_SWA || a->scenario > SAS_SCFA) return set_error(SAS_EINVAL, "bwd: bad scenario");
+  if (a->q_dtype != SAS_DT_BF16 && a->q_dtype != SAS_DT_FP16) return set_error(SAS_EINVAL, "bwd: q dtype");
+  if (a->kv_dtype != a->q_dtype) return set_error(SAS_EINVAL, "bwd: the cache must be in the query dtype (no fp8 rows)");
+  if (a->win_left < 0 || a->win_left > 8191) return set_error(SAS_EINVAL, "bwd: win_left out of range");
+  if (a->scenario >= SAS_CFA && (a->cmp_ratio < 1 || a->K < 0)) return set_error(SAS_EINVAL, "bwd: bad cmp_ratio/K");
+  const long long nslots = a->win_left + 1 + (a->scenario >= SAS_CFA ? a->K : 0);
+  if (nslots > kMaxSlots) return set_error(SAS_EINVAL, "bwd: at most %d key slots per token (got %lld)", kMaxSlots, nslots);
+  if (a->T == 0) return SAS_OK;
+  if (!a->q || !a->ori_kv || !a->ori_block_table || !a->q_prefix || !a->act_q || !a->act_kv || !a->sinks ||
+      !a->out || !a->lse || !ba->dout || !ba->dq || !ba->d_ori_kv || !ba->d_sinks)
+    return set_error(SAS_EINVAL, "bwd: null device pointer");
+  if (a->scenario >= SAS_CFA && (!a->cmp_kv || !a->cmp_block_table || !ba->d_cmp_kv))
+    return set_error(SAS_EINVAL, "bwd: CFA/SCFA need cmp_kv, cmp_block_table and d_cmp_kv");
+  if (a->scenario == SAS_SCFA && !a->cmp_indices) return set_error(SAS_EINVAL, "bwd: SCFA needs cmp_indices");
+  if (a->ori_block_size < 1 || a->ori_bt_stride < 1 || a->ori_num_blocks < 1)
+    return set_error(SAS_EINVAL, "bwd: bad ori cache geometry");
+  if (a->scenario >= SAS_CFA && (a->cmp_block_size < 1 || a->cmp_bt_stride < 1 || a->cmp_num_blocks < 1))
+    return set_error(SAS_EINVAL, "bwd: bad cmp cache geometry");
+  if ((double)a->ori_num_blocks * a->ori_block_size > 2147483000.0 ||
+      (double)a->cmp_num_blocks * std::max<int64_t>(a->cmp_block_size, 1) > 2147483000.0)
+    return set_error(SAS_EINVAL, "bwd: cache has more than 2^31 rows");
+
+  BwdParams bp{};
+  FwdParams& fp = bp.f;
+  fp.q = (const uint8_t*)a->q;
+  fp.ori_kv = (const uint8_t*)a->ori_kv;
+  fp.ori_bt = a->ori_block_table;
+  fp.cmp_kv = (const uint8_t*)a->cmp_kv;
+  fp.cmp_bt = a->cmp_block_table;
+  fp.cmp_idx = a->cmp_indices;
+  fp.q_prefix = a->q_prefix;
+  fp.act_q = a->act_q;
+  fp.act_kv = a->act_kv;
+  fp.sinks = a->sinks;
+  fp.lse = a->lse;
+  fp.T = (int)a->T; fp.B = (int)a->B; fp.H = (int)a->H;
+  fp.ori_bs = (int)a->ori_block_size; fp.ori_bt_stride = (int)a->ori_bt_stride;
+  fp.ori_nblocks = (int)a->ori_num_blocks;
+  fp.cmp_bs = (int)std::max<int64_t>(a->cmp_block_size, 1);
+  fp.cmp_bt_stride = (int)std::max<int64_t>(a->cmp_bt_stride, 1);
+  fp.cmp_nblocks = (int)a->cmp_num_blocks;
+  fp.K = (int)a->K; fp.scenario = a->scenario;
+  fp.cmp_ratio = std::max(1, a->cmp_ratio); fp.win_left = a->win_left;
+  fp.scale_log2 = a->softmax_scale * kLog2e;
+  fp.nsplit = 1; fp.slots_per_split = (int)nslots; fp.nhg = (int)a->H / 16;
+  bp.out = (const uint8_t*)a->out;
+  bp.dout = (const uint8_t*)ba->dout;
+  bp.dq = ba->dq;
+  bp.d_ori = ba->d_ori_kv;
+  bp.d_cmp = ba->d_cmp_kv;
+  bp.d_sinks = ba->d_sinks;
+  const int nblocks = (int)((a->T + kXcds - 1) / kXcds) * fp.nhg * kXcds;
+  hipStream_t st = (hipStream_t)stream;
+  if (a->q_dtype == SAS_DT_BF16)
+    return a->D == 576 ? launch_bwd<576, __bf16>(bp, nblocks, st) : launch_bwd<512, __bf16>(bp, nblocks, st);
+  return a->D == 576 ? launch_bwd<576, _Float16>(bp, nblocks, st) : launch_bwd<512, _Float16>(bp, nblocks, st);
+}

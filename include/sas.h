@@ -167,6 +167,33 @@ typedef struct SasCombineArgs {
 int sas_combine_v1(const SasCombineArgs* a, void* stream);
 
 /*
+ * Backward of sas_fwd_v1 (no counterpart launched by the reference, whose
+ * LSE output is documented as the input of a FlashAttention-v2 style
+ * backward, api.py:32-35, 176-184). `fwd` holds the forward's arguments:
+ * q, caches (in the query dtype; fp8 rows are not differentiated), tables,
+ * indices, seqlens, sinks, and its outputs `out` / `lse`, which are inputs
+ * here; its workspace / split / wave fields are ignored. Over the forward's
+ * key set J of each (token, head), with P_j = exp(scale q.k_j - lse),
+ * Delta = dout . out, dS_j = P_j (dout . v_j - Delta):
+ *   dq = scale sum_j dS_j k_j                      (written)
+ *   d_kv[row j] += scale dS_j q + [P_j dout, 0]    (accumulated, V = the first DV channels)
+ *   d_sinks[h] += -exp(sink_h - lse) Delta         (accumulated)
+ * The accumulated buffers must be zeroed by the caller first; rows of the
+ * two caches receive atomic fp32 adds, so their summation order varies.
+ * At most 1280 key slots per token (win_left + 1 + K).
+ */
+typedef struct SasBwdArgs {
+  SasFwdArgs fwd;
+  const void* dout;              /* [T, H, DV] q_dtype */
+  float* dq;                     /* [T, H, D] fp32 */
+  float* d_ori_kv;               /* [ori_num_blocks, ori_block_size, 1, D] fp32 */
+  float* d_cmp_kv;               /* [cmp_num_blocks, cmp_block_size, 1, D] fp32; NULL for SWA */
+  float* d_sinks;                /* [H] fp32 */
+} SasBwdArgs;
+
+int sas_bwd_v1(const SasBwdArgs* a, void* stream);
+
+/*
  * Paged-KV cache writer (no counterpart in the reference, whose tests build
  * paged caches on the host in the layout of golden.py:315-408; this is the
  * device-side producer of that layout). Input row r (of N) goes to the cache

@@ -1,0 +1,175 @@
+"""Backward (sas_bwd_v1): the fp64 autograd oracle pinned by the golden
+forward, finite differences and the closed-form sink gradient; the GPU
+kernel against the oracle."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dsv4_amd import cases, paged
+from oracle import backward_ref as BR
+from oracle import golden_ref as O
+
+
+def _tiny(dtype=torch.float64, seed=0, scenario=3):
+    """2 batches (q_lens 3 and 1, kv_lens 40 and 23), H = 2, D = 576, block
+    size 8, window 15, ratio 4, top-k 6: every kind of row in a few keys."""
+    g = torch.Generator().manual_seed(seed)
+    q_lens, kv_lens, bs, H, D, K, ratio = [3, 1], [40, 23], 8, 2, 576, 6, 4
+    T = sum(q_lens)
+    ori_bt, ori_nb = paged.random_block_table(kv_lens, bs, g, extra_blocks=2)
+    cmp_lens = [k // ratio for k in kv_lens]
+    cmp_bt, cmp_nb = paged.random_block_table(cmp_lens, bs, g, extra_blocks=1)
+    kw = dict(
+        ori_kv=torch.randn(ori_nb, bs, 1, D, generator=g).to(dtype), ori_block_table=ori_bt,
+        cu_seqlens_q=torch.tensor([0] + np.cumsum(q_lens).tolist(), dtype=torch.int32),
+        seqused_kv=torch.tensor(kv_lens, dtype=torch.int32), sinks=torch.randn(H, generator=g).double(),
+        softmax_scale=1 / math.sqrt(D), ori_win_left=15, dv=512)
+    if scenario >= 2:
+        kw.update(cmp_kv=torch.randn(cmp_nb, bs, 1, D, generator=g).to(dtype), cmp_block_table=cmp_bt,
+                  cmp_ratio=ratio)
+    if scenario == 3:
+        kw["cmp_sparse_indices"] = cases.topk_indices(q_lens, kv_lens, K, ratio, g)
+    q = torch.randn(T, H, D, generator=g).to(dtype)
+    dout = torch.randn(T, H, 512, generator=g).to(dtype)
+    return q, dout, kw
+
+
+def test_oracle_forward_is_golden():
+    q, dout, kw = _tiny()
+    r = BR.backward_paged(q, dout, **kw)
+    g = dict(kw)
+    g.pop("dv")
+    out, lse = O.golden_paged(q, dv=512, exact=True, **g)
+    torch.testing.assert_close(r["out"], out, atol=1e-10, rtol=1e-10)
+    torch.testing.assert_close(r["lse"], lse, atol=1e-10, rtol=1e-10)
+
+
+def test_oracle_planted_dropped_sink_fails():
+    q, dout, kw = _tiny()
+    r = BR.backward_paged(q, dout, drop_sink=True, **kw)
+    g = dict(kw)
+    g.pop("dv")
+    out, _ = O.golden_paged(q, dv=512, exact=True, **g)
+    assert not torch.allclose(r["out"], out, atol=1e-6, rtol=1e-6)
+
+
+def test_oracle_sink_gradient_closed_form():
+    """d(sink_h) = -sum_t exp(sink_h - lse_th) (dO_th . O_th): the sink's value
+    row is zero, so only the softmax normaliser depends on it."""
+    q, dout, kw = _tiny()
+    r = BR.backward_paged(q, dout, **kw)
+    delta = (dout.double() * r["out"]).sum(-1)                       # [T, H]
+    ref = -(torch.exp(kw["sinks"].view(1, -1) - r["lse"]) * delta).sum(0)
+    torch.testing.assert_close(r["d_sinks"], ref, atol=1e-12, rtol=1e-10)
+
+
+@pytest.mark.parametrize("scenario", [1, 2, 3])
+def test_oracle_finite_differences(scenario):
+    """Central differences of sum(dO * out) in fp64 match the autograd
+    gradients of q, of cache rows (a V channel and a rope channel) and of the
+    sinks."""
+    q, dout, kw = _tiny(scenario=scenario, seed=scenario)
+    r = BR.backward_paged(q, dout, **kw)
+    eps = 1e-6
+
+    def loss(qq=q, sinks=kw["sinks"], ori=kw["ori_kv"], cmp_=kw.get("cmp_kv")):
+        k2 = dict(kw, sinks=sinks, ori_kv=ori)
+        if cmp_ is not None:
+            k2["cmp_kv"] = cmp_
+        return BR.loss_fp64(qq, dout, **{k: v for k, v in k2.items() if k not in ("sinks", "ori_kv", "cmp_kv")},
+                            sinks=k2["sinks"], ori_kv=k2["ori_kv"], cmp_kv=k2.get("cmp_kv"))
+
+    def fd(name, tensor, index):
+        hi, lo = tensor.clone(), tensor.clone()
+        hi[index] += eps
+        lo[index] -= eps
+        return (loss(**{name: hi}) - loss(**{name: lo})) / (2 * eps)
+
+    for t, h, c in [(0, 0, 3), (2, 1, 511), (3, 0, 570)]:
+        assert abs(fd("qq", q, (t, h, c)) - float(r["dq"][t, h, c])) < 1e-6
+    rows, grads = r["d_ori"]
+    D = q.shape[-1]
+    for i in (0, len(rows) // 2, len(rows) - 1):
+        row = int(rows[i])
+        for c in (5, 530):
+            ix = (row // kw["ori_kv"].shape[1], row % kw["ori_kv"].shape[1], 0, c)
+            assert abs(fd("ori", kw["ori_kv"], ix) - float(grads[i, c])) < 1e-6
+    if scenario >= 2:
+        rows, grads = r["d_cmp"]
+        row = int(rows[0])
+        ix = (row // kw["cmp_kv"].shape[1], row % kw["cmp_kv"].shape[1], 0, 100)
+        assert abs(fd("cmp_", kw["cmp_kv"], ix) - float(grads[0, 100])) < 1e-6
+    for h in range(2):
+        assert abs(fd("sinks", kw["sinks"], (h,)) - float(r["d_sinks"][h])) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# GPU: the kernel against the oracle
+# ---------------------------------------------------------------------------
+
+def _gpu_case(name):
+    from tests.test_gpu_parity import _small
+    if name == "C1":
+        return cases.make_inputs(cases.CONFIGS["C1"], device="cpu")
+    spec = {
+        "scfa_prefill": dict(B=2, H=32, q_lens=[40, 3], kv_lens=[300, 90], K=64, bs=16),
+        "swa": dict(B=3, H=16, q_lens=[1, 5, 2], kv_lens=[50, 700, 128], K=0, scenario=1),
+        "cfa": dict(B=2, H=16, q_lens=[2, 1], kv_lens=[500, 333], K=0, scenario=2, ratio=8),
+        "fp16_d512": dict(B=2, H=16, q_lens=[1, 2], kv_lens=[900, 400], K=64, D=512, dtype=torch.float16),
+        "decode_h64": dict(B=8, H=64, q_lens=[1] * 8, kv_lens=[4000, 900, 129, 2500, 60, 3000, 1000, 2048], K=128),
+    }[name]
+    return _small(**spec)
+
+
+def _rel_err(got, ref):
+    ref = ref.double()
+    return float((got.double() - ref).abs().max() / max(float(ref.abs().max()), 1e-30))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["C1", "scfa_prefill", "swa", "cfa", "fp16_d512", "decode_h64"])
+def test_gpu_backward_matches_oracle(name):
+    from dsv4_amd.api import sparse_attn_sharedkv, sparse_attn_sharedkv_backward
+    inp = _gpu_case(name)
+    c = inp.cfg
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    out, lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+    g = torch.Generator().manual_seed(5)
+    dout = torch.randn(out.shape, generator=g).to(inp.q.dtype)
+    dq, d_ori, d_cmp, d_sinks = sparse_attn_sharedkv_backward(dout.cuda(), d.q, out, lse, **kw)
+    torch.cuda.synchronize()
+    r = BR.backward_paged(
+        inp.q, dout, ori_kv=inp.ori_kv, ori_block_table=inp.ori_bt, cu_seqlens_q=inp.cu_seqlens_q,
+        seqused_kv=inp.seqused_kv, sinks=inp.sinks, softmax_scale=c.scale,
+        cmp_kv=inp.cmp_kv if c.scenario >= 2 else None, cmp_block_table=inp.cmp_bt if c.scenario >= 2 else None,
+        cmp_sparse_indices=inp.cmp_idx if c.scenario == 3 else None, cmp_ratio=c.cmp_ratio,
+        ori_win_left=c.win_left)
+    D = inp.q.shape[-1]
+    errs = {"dq": _rel_err(dq.cpu(), r["dq"])}
+    rows, grads = r["d_ori"]
+    flat = d_ori.cpu().reshape(-1, D)
+    errs["d_ori"] = _rel_err(flat[rows], grads)
+    untouched = torch.ones(flat.shape[0], dtype=torch.bool)
+    untouched[rows] = False
+    assert float(flat[untouched].abs().max()) == 0.0 if untouched.any() else True
+    if c.scenario >= 2:
+        rows, grads = r["d_cmp"]
+        cflat = d_cmp.cpu().reshape(-1, D)
+        if rows.numel():
+            errs["d_cmp"] = _rel_err(cflat[rows], grads)
+        untouched = torch.ones(cflat.shape[0], dtype=torch.bool)
+        untouched[rows] = False
+        if untouched.any():
+            assert float(cflat[untouched].abs().max()) == 0.0
+    errs["d_sinks"] = _rel_err(d_sinks.cpu(), r["d_sinks"])
+    print(f"[bwd] {name}: max|err| / max|ref| = {errs}", flush=True)
+    # tolerance: bf16 / fp16 rounding of the forward output (used in Delta)
+    # and of dq; fp32 accumulation everywhere else
+    for k_, e in errs.items():
+        assert e < 2e-2, f"{name} {k_}: relative error {e:.3g}"
