@@ -248,6 +248,37 @@ def bench_cache_write(traffic=None):
                 _log=f"cache write: {us:.2f} us/call, {gbs:.0f} GB/s ({byts} B)")
 
 
+BWD_FLOP_PER_PAIR_HEAD = 2 * (3 * 576 + 2 * 512)   # q.k, dO.v, dq, dk (D = 576), dv (512)
+
+
+def bench_backward(dec_inp, pre_inp):
+    """sas_bwd_v1 on the C2 decode and C3 prefill inputs: the forward's out /
+    LSE, a random bf16 dO, gradient buffers allocated once (the kernel's own
+    time: the cache gradients accumulate across the timed launches). Useful
+    FLOP per (token, key, head): 2 x (3 x 576 + 2 x 512) = 5504."""
+    from dsv4_amd import cases
+    from dsv4_amd.api import prepare_sparse_attn_sharedkv_backward, sparse_attn_sharedkv
+    res = {"kernel": "sas_bwd_kernel (VALU fp32, first version)",
+           "flop_per_pair_head": BWD_FLOP_PER_PAIR_HEAD}
+    for key, inp, steps in (("decode", dec_inp, 50), ("prefill", pre_inp, 3)):
+        if inp is None:
+            continue
+        kw = inp.api_kwargs()
+        out, lse = sparse_attn_sharedkv(inp.q, return_softmax_lse=True, **kw)
+        g = torch.Generator(device="cuda").manual_seed(21)
+        dout = torch.randn(out.shape, device="cuda", generator=g).to(out.dtype)
+        pb = prepare_sparse_attn_sharedkv_backward(dout, inp.q, out, lse, **kw)
+        ms, _ = time_launches(lambda i, st: pb.launch(st), 1, steps, 1)
+        us = ms * 1e3 / steps
+        pairs = cases.gathered_rows(inp)
+        flop = pairs * inp.cfg.H * BWD_FLOP_PER_PAIR_HEAD
+        tfl = flop / (us * 1e-6) / 1e12
+        res[key] = dict(workload=inp.cfg.name, us_per_call=round(us, 1), useful_flop=flop,
+                        tflops=round(tfl, 2), mfma_frac=round(tfl / BF16_PEAK_TFLOPS, 5))
+        del pb, out, lse, dout
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -259,6 +290,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-traffic", action="store_true")
     ap.add_argument("--no-cache-write", action="store_true")
+    ap.add_argument("--no-backward", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -351,6 +383,15 @@ def main():
                        mfma_frac=round(tfl / BF16_PEAK_TFLOPS, 4), splits=pcall.num_splits)
         log(f"C3 prefill: {pus:.1f} us/call, {tfl:.1f} TFLOP/s ({flops:.4e} useful FLOP)")
 
+    # ---------------- backward (C2 decode, C3 prefill) ----------------------
+    backward = None
+    if not args.no_backward:
+        backward = bench_backward(inp, pinp if prefill is not None else None)
+        for k_ in ("decode", "prefill"):
+            if backward.get(k_):
+                log(f"backward {k_}: {backward[k_]['us_per_call']:.1f} us/call, "
+                    f"{backward[k_]['tflops']:.1f} TFLOP/s")
+
     # ---------------- paged-KV cache writer (fp8 rows) ------------------------
     cwrite = None
     if not args.no_cache_write:
@@ -409,6 +450,7 @@ def main():
                      "traffic_detail": traffic if traffic else traffic_note},
         "prefill": prefill,
         "cache_write": cwrite,
+        "backward": backward,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -377,6 +377,60 @@ def sparse_attn_sharedkv(
     return call.result(return_softmax_lse)
 
 
+class PreparedBackward:
+    """Arguments and gradient buffers of one backward, resolved once;
+    :meth:`launch` enqueues the kernel (the gradients accumulate:
+    :meth:`zero_grads` clears them), :meth:`result` returns them."""
+
+    def __init__(self, call: PreparedCall, ba, keep, q, dq, d_ori, d_cmp, d_sinks):
+        self._call, self.args, self._keep, self._q = call, ba, keep, q
+        self.dq, self.d_ori_kv, self.d_cmp_kv, self.d_sinks = dq, d_ori, d_cmp, d_sinks
+
+    def launch(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+        _lib.check(_lib.lib().sas_bwd_v1(C.byref(self.args), self._call._stream(stream)),
+                   "sparse_attn_sharedkv_backward")
+
+    def zero_grads(self) -> None:
+        for t in (self.dq, self.d_ori_kv, self.d_cmp_kv, self.d_sinks):
+            if t is not None:
+                t.zero_()
+
+    def result(self):
+        return (self.dq.to(self._q.dtype).reshape(self._q.shape), self.d_ori_kv, self.d_cmp_kv,
+                self.d_sinks)
+
+
+def prepare_sparse_attn_sharedkv_backward(dout: torch.Tensor, q: torch.Tensor, out: torch.Tensor,
+                                          lse: torch.Tensor, **kwargs) -> PreparedBackward:
+    """Validate and bind the arguments of :func:`sparse_attn_sharedkv_backward`
+    and allocate its (zeroed) gradient buffers."""
+    kwargs.pop("return_softmax_lse", None)
+    call = prepare_sparse_attn_sharedkv(q, **kwargs)
+    a = call.args
+    if a.kv_dtype != a.q_dtype:
+        raise ValueError("the backward needs caches in the query dtype (fp8 rows are not differentiated)")
+    T1, H = int(a.T), int(a.H)
+    dev = q.device
+    dout_f = dout.reshape(T1, H, 512)
+    out_f = out.reshape(T1, H, 512)
+    lse_f = lse.reshape(T1, H)
+    for name, t_, dt in (("dout", dout_f, q.dtype), ("out", out_f, q.dtype), ("lse", lse_f, torch.float32)):
+        if t_.dtype != dt or t_.device != dev:
+            raise ValueError(f"{name} must be a {dt} tensor on {dev}")
+    dout_f, out_f, lse_f = dout_f.contiguous(), out_f.contiguous(), lse_f.contiguous()
+    ori_kv = kwargs["ori_kv"]
+    cmp_kv = kwargs.get("cmp_kv")
+    dq = torch.zeros((T1, H, int(a.D)), dtype=torch.float32, device=dev)
+    d_ori = torch.zeros(ori_kv.shape, dtype=torch.float32, device=dev)
+    d_cmp = torch.zeros(cmp_kv.shape, dtype=torch.float32, device=dev) if cmp_kv is not None else None
+    d_sinks = torch.zeros(H, dtype=torch.float32, device=dev)
+    a.out, a.lse = out_f.data_ptr(), lse_f.data_ptr()
+    ba = _lib.SasBwdArgs(fwd=a, dout=dout_f.data_ptr(), dq=dq.data_ptr(), d_ori_kv=d_ori.data_ptr(),
+                         d_cmp_kv=d_cmp.data_ptr() if d_cmp is not None else None,
+                         d_sinks=d_sinks.data_ptr())
+    return PreparedBackward(call, ba, [dout_f, out_f, lse_f], q, dq, d_ori, d_cmp, d_sinks)
+
+
 def sparse_attn_sharedkv_backward(
     dout: torch.Tensor,
     q: torch.Tensor,
@@ -396,29 +450,6 @@ def sparse_attn_sharedkv_backward(
     ``[H]``. Key sets are the forward's: window rows and the valid top-k (or
     dense compressed) rows; V is the first 512 channels of each row.
     """
-    kwargs.pop("return_softmax_lse", None)
-    call = prepare_sparse_attn_sharedkv(q, **kwargs)
-    a = call.args
-    if a.kv_dtype != a.q_dtype:
-        raise ValueError("the backward needs caches in the query dtype (fp8 rows are not differentiated)")
-    T1, H = int(a.T), int(a.H)
-    dev = q.device
-    dout_f = dout.reshape(T1, H, 512)
-    out_f = out.reshape(T1, H, 512)
-    lse_f = lse.reshape(T1, H)
-    for name, t_, dt in (("dout", dout_f, q.dtype), ("out", out_f, q.dtype), ("lse", lse_f, torch.float32)):
-        if t_.dtype != dt or t_.device != dev:
-            raise ValueError(f"{name} must be a {dt} tensor on {dev}")
-    dout_f, out_f, lse_f = dout_f.contiguous(), out_f.contiguous(), lse_f.contiguous()
-    ori_kv = kwargs["ori_kv"]
-    cmp_kv = kwargs.get("cmp_kv")
-    dq = torch.empty((T1, H, int(a.D)), dtype=torch.float32, device=dev)
-    d_ori = torch.zeros(ori_kv.shape, dtype=torch.float32, device=dev)
-    d_cmp = torch.zeros(cmp_kv.shape, dtype=torch.float32, device=dev) if cmp_kv is not None else None
-    d_sinks = torch.zeros(H, dtype=torch.float32, device=dev)
-    a.out, a.lse = out_f.data_ptr(), lse_f.data_ptr()
-    ba = _lib.SasBwdArgs(fwd=a, dout=dout_f.data_ptr(), dq=dq.data_ptr(), d_ori_kv=d_ori.data_ptr(),
-                         d_cmp_kv=d_cmp.data_ptr() if d_cmp is not None else None,
-                         d_sinks=d_sinks.data_ptr())
-    _lib.check(_lib.lib().sas_bwd_v1(C.byref(ba), call._stream(None)), "sparse_attn_sharedkv_backward")
-    return dq.to(q.dtype).reshape(q.shape), d_ori, d_cmp, d_sinks
+    pb = prepare_sparse_attn_sharedkv_backward(dout, q, out, lse, **kwargs)
+    pb.launch()
+    return pb.result()

@@ -13,16 +13,20 @@
 //   dkv_j += scale dS_j q  +  [P_j dO, 0]   (summed over heads and tokens)
 //   dsink += -P_sink Delta                   (the sink's value row is zero)
 //
-// One workgroup (4 waves) per (token, 16-head group). Thread (h, part) keeps
+// One workgroup (4 waves) per (token, 16-head group, KV split). With few
+// tokens the token's key slots are split over several workgroups (as in the
+// forward), which then add their dq shares atomically. Thread (h, part) keeps
 // q, dO of head h for channel part `part` (D / 16 channels) in registers and
 // accumulates that part of dq. Rows stream through LDS in chunks of 16: each
-// thread's partial q.k and dO.v sums are reduce-scattered over the head's 16
-// lanes so lane `part` ends with row `part`'s score, computes P and dS, and
-// shares them through LDS; then every thread adds dS k to its dq part and
-// owns up to three channels of the chunk's dkv rows (a sum over the 16
-// heads, added to the fp32 gradient cache rows with atomics). VALU only:
+// thread's partial q.k and dO.v sums are summed over the head's 16 lanes
+// (DPP row permutes), lane `part` computes row `part`'s P and dS and shares
+// them through LDS; then every thread adds dS k to its dq part and owns up
+// to two channel pairs of the chunk's dkv rows (a sum over the 16 heads,
+// added to the fp32 gradient cache rows with atomics). VALU only:
 // a first, exact version; the forward's MFMA layouts are the way to speed
 // it up.
+
+#include <type_traits>
 
 #include "sas_kern.h"
 
@@ -46,25 +50,31 @@ __device__ __forceinline__ float to_f(uint16_t v) {
   return (float)__builtin_bit_cast(QT, v);
 }
 
-// Butterfly reduce-scatter over the 16 lanes of a head: lane `part` returns
-// the lane-sum of v[part].
-__device__ __forceinline__ float reduce_scatter16(float (&v)[kBwdRows], int part) {
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) {
-    const bool up = part & o;
-#pragma unroll
-    for (int i = 0; i < o; ++i) {
-      const float send = up ? v[i] : v[i + o];
-      const float keep = up ? v[i + o] : v[i];
-      v[i] = keep + __shfl_xor(send, o);
-    }
-  }
-  return v[0];
+// c + a.x * b.x + a.y * b.y for two packed 16-bit pairs (v_dot2c_f32_bf16 /
+// v_dot2c_f32_f16)
+template <typename QT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  typedef QT v2 __attribute__((ext_vector_type(2)));
+  if constexpr (std::is_same<QT, __bf16>::value)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
 }
 
+// two packed 16-bit values (low half first) -> floats
+template <typename QT>
+__device__ __forceinline__ float2 unpack2(uint32_t w) {
+  return make_float2(to_f<QT>((uint16_t)(w & 0xffffu)), to_f<QT>((uint16_t)(w >> 16)));
+}
+
+// Sum over the 16 lanes of a DPP row (a head's lanes), returned in every
+// lane: quad_perm [1,0,3,2] and [2,3,0,1] (lane xor 1, xor 2), then
+// row_half_mirror and row_mirror pair the quads and the halves.
 __device__ __forceinline__ float sum16(float x) {
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));
   return x;
 }
 
@@ -88,29 +98,34 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
   const int hq = k.hg * 16 + h;
   const int t = k.t;
   float* dqp = bp.dq + ((size_t)t * p.H + hq) * D + part * CP;
-  if (k.padded) {
-#pragma unroll
-    for (int i = 0; i < CP; ++i) dqp[i] = 0.f;
+  if (k.padded) {   // dq stays zero (the caller zeroes it)
     return;
   }
 
-  // this thread's q / dO / O channels, Delta, and the tiles for the dkv phase
-  const uint16_t* qg = reinterpret_cast<const uint16_t*>(p.q) + ((size_t)t * p.H + hq) * D + part * CP;
-  const uint16_t* dog = reinterpret_cast<const uint16_t*>(bp.dout) + ((size_t)t * p.H + hq) * kDV;
-  const uint16_t* og = reinterpret_cast<const uint16_t*>(bp.out) + ((size_t)t * p.H + hq) * kDV;
-  float qr[CP], dr[CP], dq[CP];
+  // this thread's q / dO channels as packed pairs (dO zero past channel
+  // 512), Delta = dO . O over the head's 16 lanes
+  const uint32_t* qg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(p.q) +
+                                                         ((size_t)t * p.H + hq) * D + part * CP);
+  const uint32_t* dog = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(bp.dout) +
+                                                          ((size_t)t * p.H + hq) * kDV);
+  const uint32_t* og = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(bp.out) +
+                                                         ((size_t)t * p.H + hq) * kDV);
+  constexpr int CP2 = CP / 2;
+  uint32_t qr[CP2], dr[CP2];
+  float dq[CP];
   float dpart = 0.f;
 #pragma unroll
-  for (int i = 0; i < CP; ++i) {
-    const int c = part * CP + i;
-    qr[i] = to_f<QT>(qg[i]);
-    dr[i] = c < kDV ? to_f<QT>(dog[c]) : 0.f;
-    if (c < kDV) dpart += dr[i] * to_f<QT>(og[c]);
-    dq[i] = 0.f;
+  for (int i = 0; i < CP2; ++i) {
+    const int c2 = part * CP2 + i;   // channel pair
+    qr[i] = qg[i];
+    dr[i] = 2 * c2 < kDV ? dog[c2] : 0u;
+    if (2 * c2 < kDV) dpart = dot2<QT>(dr[i], og[c2], dpart);
   }
+#pragma unroll
+  for (int i = 0; i < CP; ++i) dq[i] = 0.f;
   const float delta = sum16(dpart);
   const float lse2 = p.lse[(size_t)t * p.H + hq] * kLog2e;
-  if (part == 0) {
+  if (part == 0 && k.sp == 0) {
     const float psink = __builtin_amdgcn_exp2f(p.sinks[hq] * kLog2e - lse2);
     atomicAdd(bp.d_sinks + hq, -psink * delta);
   }
@@ -138,19 +153,27 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
     float sv[kBwdRows], dv[kBwdRows];
 #pragma unroll
     for (int r = 0; r < kBwdRows; ++r) {
-      const uint16_t* kr = reinterpret_cast<const uint16_t*>(lds_k + r * KS) + part * CP;
+      const uint2* kr = reinterpret_cast<const uint2*>(lds_k + r * KS + part * CP * 2);
       float s = 0.f, d = 0.f;
 #pragma unroll
-      for (int i = 0; i < CP; ++i) {
-        const float kv = to_f<QT>(kr[i]);
-        s += qr[i] * kv;
-        d += dr[i] * kv;   // dr is zero past channel 512
+      for (int i = 0; i < CP / 4; ++i) {
+        const uint2 w = kr[i];
+        s = dot2<QT>(qr[2 * i], w.x, s);
+        s = dot2<QT>(qr[2 * i + 1], w.y, s);
+        d = dot2<QT>(dr[2 * i], w.x, d);       // dr is zero past channel 512
+        d = dot2<QT>(dr[2 * i + 1], w.y, d);
       }
       sv[r] = s;
       dv[r] = d;
     }
-    const float s_row = reduce_scatter16(sv, part);    // row `part`
-    const float dp_row = reduce_scatter16(dv, part);
+    // every lane of the head gets each row's sums; lane `part` keeps row `part`
+    float s_row = 0.f, dp_row = 0.f;
+#pragma unroll
+    for (int r = 0; r < kBwdRows; ++r) {
+      const float a = sum16(sv[r]), b = sum16(dv[r]);
+      s_row = r == part ? a : s_row;
+      dp_row = r == part ? b : dp_row;
+    }
     float pr = 0.f, dsr = 0.f;
     if (part < nr) {
       pr = __builtin_amdgcn_exp2f(s_row * p.scale_log2 - lse2);
@@ -162,32 +185,53 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
     // dq part += sum_r scale dS_r k_r
     for (int r = 0; r < nr; ++r) {
       const float w = lds_pd[r][h][1];
-      const uint16_t* kr = reinterpret_cast<const uint16_t*>(lds_k + r * KS) + part * CP;
+      const uint2* kr = reinterpret_cast<const uint2*>(lds_k + r * KS + part * CP * 2);
 #pragma unroll
-      for (int i = 0; i < CP; ++i) dq[i] += w * to_f<QT>(kr[i]);
+      for (int i = 0; i < CP / 4; ++i) {
+        const uint2 u = kr[i];
+        const float2 a = unpack2<QT>(u.x), b = unpack2<QT>(u.y);
+        dq[4 * i] += w * a.x; dq[4 * i + 1] += w * a.y; dq[4 * i + 2] += w * b.x; dq[4 * i + 3] += w * b.y;
+      }
     }
-    // dkv rows of the chunk: channel c = tid + 256 m, summed over the heads
+    // dkv rows of the chunk: channel pair cp = tid + 256 m (channels 2 cp,
+    // 2 cp + 1), summed over the 16 heads
     for (int r = 0; r < nr; ++r) {
       const uint64_t a = lds_rows[c0 + r];
       float* g = a - ori_lo < ori_n ? bp.d_ori + (a - ori_lo) / (D * 2) * D
                                     : bp.d_cmp + (a - cmp_lo) / (D * 2) * D;
+      float pv[16], dsv[16];
 #pragma unroll
-      for (int m = 0; m < (D + 255) / 256; ++m) {
-        const int c = tid + 256 * m;
-        if (c >= D) break;
-        float acc = 0.f;
+      for (int hh = 0; hh < 16; ++hh) { pv[hh] = lds_pd[r][hh][0]; dsv[hh] = lds_pd[r][hh][1]; }
+#pragma unroll
+      for (int m = 0; m < (D / 2 + 255) / 256; ++m) {
+        const int cp = tid + 256 * m;
+        if (cp >= D / 2) break;
+        float a0 = 0.f, a1 = 0.f;
 #pragma unroll
         for (int hh = 0; hh < 16; ++hh) {
-          acc += lds_pd[r][hh][1] * to_f<QT>(lds_q[hh * D + c]);
-          if (c < kDV) acc += lds_pd[r][hh][0] * to_f<QT>(lds_do[hh * kDV + c]);
+          const float2 qv = unpack2<QT>(reinterpret_cast<const uint32_t*>(lds_q + hh * D)[cp]);
+          a0 += dsv[hh] * qv.x;
+          a1 += dsv[hh] * qv.y;
+          if (2 * cp < kDV) {
+            const float2 ov = unpack2<QT>(reinterpret_cast<const uint32_t*>(lds_do + hh * kDV)[cp]);
+            a0 += pv[hh] * ov.x;
+            a1 += pv[hh] * ov.y;
+          }
         }
-        atomicAdd(g + c, acc);
+        atomicAdd(g + 2 * cp, a0);
+        atomicAdd(g + 2 * cp + 1, a1);
       }
     }
     __syncthreads();
   }
+  // one split: the workgroup owns the head's dq; several: each adds its share
+  if (p.nsplit == 1) {
 #pragma unroll
-  for (int i = 0; i < CP; ++i) dqp[i] = dq[i];
+    for (int i = 0; i < CP; ++i) dqp[i] = dq[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < CP; ++i) atomicAdd(dqp + i, dq[i]);
+  }
 }
 
 template <int D, typename QT>
@@ -253,14 +297,26 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   fp.K = (int)a->K; fp.scenario = a->scenario;
   fp.cmp_ratio = std::max(1, a->cmp_ratio); fp.win_left = a->win_left;
   fp.scale_log2 = a->softmax_scale * kLog2e;
-  fp.nsplit = 1; fp.slots_per_split = (int)nslots; fp.nhg = (int)a->H / 16;
+  // KV splits: the caller's count, else enough (token, head group, split)
+  // workgroups for two per CU, each split at least 64 slots
+  fp.nhg = (int)a->H / 16;
+  int ns = a->num_splits;
+  if (ns <= 0) {
+    const long long items = a->T * fp.nhg;
+    const long long want = (2 * kCus + items - 1) / items;
+    ns = (int)std::min<long long>(want, (nslots + 63) / 64);
+  }
+  ns = std::max(1, std::min(ns, 64));
+  const int sps = (int)((nslots + ns - 1) / ns);
+  fp.nsplit = (int)((nslots + sps - 1) / sps);
+  fp.slots_per_split = sps;
   bp.out = (const uint8_t*)a->out;
   bp.dout = (const uint8_t*)ba->dout;
   bp.dq = ba->dq;
   bp.d_ori = ba->d_ori_kv;
   bp.d_cmp = ba->d_cmp_kv;
   bp.d_sinks = ba->d_sinks;
-  const int nblocks = (int)((a->T + kXcds - 1) / kXcds) * fp.nhg * kXcds;
+  const int nblocks = (int)((a->T + kXcds - 1) / kXcds) * fp.nhg * fp.nsplit * kXcds;
   hipStream_t st = (hipStream_t)stream;
   if (a->q_dtype == SAS_DT_BF16)
     return a->D == 576 ? launch_bwd<576, __bf16>(bp, nblocks, st) : launch_bwd<512, __bf16>(bp, nblocks, st);

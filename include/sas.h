@@ -172,20 +172,22 @@ int sas_combine_v1(const SasCombineArgs* a, void* stream);
  * backward, api.py:32-35, 176-184). `fwd` holds the forward's arguments:
  * q, caches (in the query dtype; fp8 rows are not differentiated), tables,
  * indices, seqlens, sinks, and its outputs `out` / `lse`, which are inputs
- * here; its workspace / split / wave fields are ignored. Over the forward's
+ * here; its workspace / head-group / wave fields are ignored, num_splits
+ * (> 0) sets the KV split count (0: chosen for >= 2 workgroups per CU). Over the forward's
  * key set J of each (token, head), with P_j = exp(scale q.k_j - lse),
  * Delta = dout . out, dS_j = P_j (dout . v_j - Delta):
- *   dq = scale sum_j dS_j k_j                      (written)
+ *   dq = scale sum_j dS_j k_j                      (zero on entry; written or accumulated)
  *   d_kv[row j] += scale dS_j q + [P_j dout, 0]    (accumulated, V = the first DV channels)
  *   d_sinks[h] += -exp(sink_h - lse) Delta         (accumulated)
- * The accumulated buffers must be zeroed by the caller first; rows of the
- * two caches receive atomic fp32 adds, so their summation order varies.
+ * All four outputs must be zeroed by the caller first; cache rows (and dq
+ * with several KV splits) receive atomic fp32 adds, so their summation order
+ * varies.
  * At most 1280 key slots per token (win_left + 1 + K).
  */
 typedef struct SasBwdArgs {
   SasFwdArgs fwd;
   const void* dout;              /* [T, H, DV] q_dtype */
-  float* dq;                     /* [T, H, D] fp32 */
+  float* dq;                     /* [T, H, D] fp32, zero on entry */
   float* d_ori_kv;               /* [ori_num_blocks, ori_block_size, 1, D] fp32 */
   float* d_cmp_kv;               /* [cmp_num_blocks, cmp_block_size, 1, D] fp32; NULL for SWA */
   float* d_sinks;                /* [H] fp32 */

@@ -173,3 +173,24 @@ def test_gpu_backward_matches_oracle(name):
     # and of dq; fp32 accumulation everywhere else
     for k_, e in errs.items():
         assert e < 2e-2, f"{name} {k_}: relative error {e:.3g}"
+
+
+@pytest.mark.gpu
+def test_gpu_backward_split_count_invariance():
+    """The key range split over 1, 3 or 7 workgroups per (token, head group)
+    (dq then accumulated atomically) gives the same gradients up to fp32
+    summation order."""
+    from dsv4_amd.api import sparse_attn_sharedkv, sparse_attn_sharedkv_backward
+    inp = _gpu_case("decode_h64")
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    out, lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+    g = torch.Generator().manual_seed(6)
+    dout = torch.randn(out.shape, generator=g).to(inp.q.dtype).cuda()
+    res = [sparse_attn_sharedkv_backward(dout, d.q, out, lse, num_splits=ns, **kw) for ns in (1, 3, 7)]
+    torch.cuda.synchronize()
+    for other in res[1:]:
+        for a_, b_ in zip(res[0], other):
+            if a_ is not None:
+                assert _rel_err(b_.float().cpu(), a_.float().cpu()) < 1e-2 if a_.dtype != torch.float32 \
+                    else _rel_err(b_.cpu(), a_.cpu()) < 1e-5
