@@ -453,3 +453,38 @@ def sparse_attn_sharedkv_backward(
     pb = prepare_sparse_attn_sharedkv_backward(dout, q, out, lse, **kwargs)
     pb.launch()
     return pb.result()
+
+
+class _SparseAttnSharedkvFn(torch.autograd.Function):
+    """Autograd binding: forward = :func:`sparse_attn_sharedkv` (keeping
+    out / LSE), backward = :func:`sparse_attn_sharedkv_backward`."""
+
+    @staticmethod
+    def forward(ctx, q, ori_kv, cmp_kv, sinks, kw):
+        kwargs = dict(kw, ori_kv=ori_kv, cmp_kv=cmp_kv, sinks=sinks)
+        out, lse = sparse_attn_sharedkv(q, return_softmax_lse=True, **kwargs)
+        ctx.save_for_backward(q, ori_kv, cmp_kv if cmp_kv is not None else torch.empty(0), sinks, out, lse)
+        ctx.kw = kw
+        ctx.has_cmp = cmp_kv is not None
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        q, ori_kv, cmp_kv, sinks, out, lse = ctx.saved_tensors
+        kwargs = dict(ctx.kw, ori_kv=ori_kv, cmp_kv=cmp_kv if ctx.has_cmp else None, sinks=sinks)
+        dq, d_ori, d_cmp, d_sinks = sparse_attn_sharedkv_backward(
+            dout.to(q.dtype).contiguous(), q, out, lse, **kwargs)
+        return (dq, d_ori.to(ori_kv.dtype), d_cmp.to(cmp_kv.dtype) if ctx.has_cmp else None,
+                d_sinks.to(sinks.dtype), None)
+
+
+def sparse_attn_sharedkv_autograd(q: torch.Tensor, *, ori_kv: torch.Tensor,
+                                  cmp_kv: Optional[torch.Tensor] = None, sinks: torch.Tensor,
+                                  return_softmax_lse: bool = False, **kwargs):
+    """:func:`sparse_attn_sharedkv` recorded for autograd: gradients flow to
+    ``q``, ``ori_kv``, ``cmp_kv`` and ``sinks`` (through
+    :func:`sparse_attn_sharedkv_backward`; the LSE output is not
+    differentiable). Other arguments as for :func:`sparse_attn_sharedkv`."""
+    out, lse = _SparseAttnSharedkvFn.apply(q, ori_kv, cmp_kv, sinks, kwargs)
+    return (out, lse) if return_softmax_lse else out

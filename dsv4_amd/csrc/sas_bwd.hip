@@ -20,11 +20,11 @@
 // accumulates that part of dq. Rows stream through LDS in chunks of 16: each
 // thread's partial q.k and dO.v sums are summed over the head's 16 lanes
 // (DPP row permutes), lane `part` computes row `part`'s P and dS and shares
-// them through LDS; then every thread adds dS k to its dq part and owns up
-// to two channel pairs of the chunk's dkv rows (a sum over the 16 heads,
-// added to the fp32 gradient cache rows with atomics). VALU only:
-// a first, exact version; the forward's MFMA layouts are the way to speed
-// it up.
+// them through LDS; then every thread adds dS k to its dq part, and the
+// chunk's dkv rows (sums over the 16 heads) come from 16x16x16 MFMAs
+// (dS . Q + P . dO per 16-channel tile) and are added to the fp32 gradient
+// cache rows with atomics. The scores and dq stay on the VALU (dot2 / FMA);
+// the forward's MFMA layouts are the way to move them too.
 
 #include <type_traits>
 
@@ -84,8 +84,9 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
   constexpr int CH = D / 8;                    // 16-byte chunks per row
   constexpr int KS = D * 2 + 16;               // LDS row stride (bytes)
   __shared__ __attribute__((aligned(16))) uint8_t lds_k[kBwdRows * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_q[16 * D];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_do[16 * kDV];
+  constexpr int QS = D * 2 + 16, OS = kDV * 2 + 16;   // padded q / dO row strides (bytes)
+  __shared__ __attribute__((aligned(16))) uint8_t lds_q[16 * QS];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_do[16 * OS];
   __shared__ float lds_pd[kBwdRows][16][2];    // (P, scale dS) per row and head
 
   const FwdParams& p = bp.f;
@@ -134,8 +135,10 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
                                                      ((size_t)t * p.H + k.hg * 16) * D);
     const uint4* ds = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(bp.dout) +
                                                      ((size_t)t * p.H + k.hg * 16) * kDV);
-    for (int i = tid; i < 16 * D / 8; i += 256) reinterpret_cast<uint4*>(lds_q)[i] = qs[i];
-    for (int i = tid; i < 16 * kDV / 8; i += 256) reinterpret_cast<uint4*>(lds_do)[i] = ds[i];
+    for (int i = tid; i < 16 * D / 8; i += 256)
+      *reinterpret_cast<uint4*>(lds_q + (i / (D / 8)) * QS + (i % (D / 8)) * 16) = qs[i];
+    for (int i = tid; i < 16 * kDV / 8; i += 256)
+      *reinterpret_cast<uint4*>(lds_do + (i / (kDV / 8)) * OS + (i % (kDV / 8)) * 16) = ds[i];
   }
   const float scale = p.scale_log2 / kLog2e;
   const uint64_t ori_lo = reinterpret_cast<uint64_t>(p.ori_kv);
@@ -193,33 +196,44 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
         dq[4 * i] += w * a.x; dq[4 * i + 1] += w * a.y; dq[4 * i + 2] += w * b.x; dq[4 * i + 3] += w * b.y;
       }
     }
-    // dkv rows of the chunk: channel pair cp = tid + 256 m (channels 2 cp,
-    // 2 cp + 1), summed over the 16 heads
-    for (int r = 0; r < nr; ++r) {
-      const uint64_t a = lds_rows[c0 + r];
-      float* g = a - ori_lo < ori_n ? bp.d_ori + (a - ori_lo) / (D * 2) * D
-                                    : bp.d_cmp + (a - cmp_lo) / (D * 2) * D;
-      float pv[16], dsv[16];
+    // dkv rows of the chunk by 16x16x16 MFMA: per 16-channel tile ct,
+    // dK[key][ch] = dS[key][head] . Q[head][ch] (+ P[key][head] . dO[head][ch]
+    // for ch < 512). A = 4 heads (4g .. 4g + 3) of key c16 from the (P, dS)
+    // table, rounded to the query dtype; B = the same 4 heads of channel
+    // 16 ct + c16 from the q / dO tiles (rows padded so the four head-row
+    // groups of a read hit distinct banks). Lane (g, c16) then holds keys
+    // 4g .. 4g + 3 of channel 16 ct + c16 and adds them to the rows' fp32
+    // gradients (64-byte runs per key).
+    {
+      const int c16 = lane & 15, g4 = lane >> 4;
+      uint2 a_ds, a_p;
+      a_ds.x = pack2<QT>(lds_pd[c16][4 * g4][1], lds_pd[c16][4 * g4 + 1][1]);
+      a_ds.y = pack2<QT>(lds_pd[c16][4 * g4 + 2][1], lds_pd[c16][4 * g4 + 3][1]);
+      a_p.x = pack2<QT>(lds_pd[c16][4 * g4][0], lds_pd[c16][4 * g4 + 1][0]);
+      a_p.y = pack2<QT>(lds_pd[c16][4 * g4 + 2][0], lds_pd[c16][4 * g4 + 3][0]);
+      float* grow[4];
 #pragma unroll
-      for (int hh = 0; hh < 16; ++hh) { pv[hh] = lds_pd[r][hh][0]; dsv[hh] = lds_pd[r][hh][1]; }
+      for (int i = 0; i < 4; ++i) {
+        const int key = 4 * g4 + i;
+        const uint64_t a = lds_rows[c0 + min(key, nr - 1)];
+        grow[i] = key < nr ? (a - ori_lo < ori_n ? bp.d_ori + (a - ori_lo) / (D * 2) * D
+                                                 : bp.d_cmp + (a - cmp_lo) / (D * 2) * D)
+                           : nullptr;
+      }
+      auto col4 = [&](const uint8_t* base, int stride, int ch) {
+        const uint32_t v0 = *reinterpret_cast<const uint16_t*>(base + (4 * g4) * stride + ch * 2);
+        const uint32_t v1 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 1) * stride + ch * 2);
+        const uint32_t v2 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 2) * stride + ch * 2);
+        const uint32_t v3 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 3) * stride + ch * 2);
+        return make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+      };
+      for (int ct = wave; ct < D / 16; ct += 4) {
+        const int ch = ct * 16 + c16;
+        f32x4 acc = mfma16k<QT>(a_ds, col4(lds_q, QS, ch), f32x4{0.f, 0.f, 0.f, 0.f});
+        if (ct < kDV / 16) acc = mfma16k<QT>(a_p, col4(lds_do, OS, ch), acc);
 #pragma unroll
-      for (int m = 0; m < (D / 2 + 255) / 256; ++m) {
-        const int cp = tid + 256 * m;
-        if (cp >= D / 2) break;
-        float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-        for (int hh = 0; hh < 16; ++hh) {
-          const float2 qv = unpack2<QT>(reinterpret_cast<const uint32_t*>(lds_q + hh * D)[cp]);
-          a0 += dsv[hh] * qv.x;
-          a1 += dsv[hh] * qv.y;
-          if (2 * cp < kDV) {
-            const float2 ov = unpack2<QT>(reinterpret_cast<const uint32_t*>(lds_do + hh * kDV)[cp]);
-            a0 += pv[hh] * ov.x;
-            a1 += pv[hh] * ov.y;
-          }
-        }
-        atomicAdd(g + 2 * cp, a0);
-        atomicAdd(g + 2 * cp + 1, a1);
+        for (int i = 0; i < 4; ++i)
+          if (grow[i]) atomicAdd(grow[i] + ch, acc[i]);
       }
     }
     __syncthreads();

@@ -194,3 +194,30 @@ def test_gpu_backward_split_count_invariance():
             if a_ is not None:
                 assert _rel_err(b_.float().cpu(), a_.float().cpu()) < 1e-2 if a_.dtype != torch.float32 \
                     else _rel_err(b_.cpu(), a_.cpu()) < 1e-5
+
+
+@pytest.mark.gpu
+def test_gpu_autograd_binding():
+    """loss.backward() through sparse_attn_sharedkv_autograd gives the
+    gradients of sparse_attn_sharedkv_backward."""
+    from dsv4_amd.api import sparse_attn_sharedkv_autograd, sparse_attn_sharedkv, sparse_attn_sharedkv_backward
+    inp = _gpu_case("scfa_prefill")
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    q = d.q.clone().requires_grad_(True)
+    ori = d.ori_kv.clone().requires_grad_(True)
+    cmp_ = d.cmp_kv.clone().requires_grad_(True)
+    snk = d.sinks.clone().requires_grad_(True)
+    rest = {k: v for k, v in kw.items() if k not in ("ori_kv", "cmp_kv", "sinks")}
+    out = sparse_attn_sharedkv_autograd(q, ori_kv=ori, cmp_kv=cmp_, sinks=snk, **rest)
+    g = torch.Generator().manual_seed(8)
+    dout = torch.randn(out.shape, generator=g).to(out.dtype).cuda()
+    (out.float() * dout.float()).sum().backward()
+    o2, lse2 = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+    ref = sparse_attn_sharedkv_backward(dout, d.q, o2, lse2, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out.detach().cpu(), o2.cpu())
+    assert _rel_err(q.grad.float().cpu(), ref[0].float().cpu()) < 1e-2
+    assert _rel_err(ori.grad.float().cpu(), ref[1].cpu()) < 1e-2
+    assert _rel_err(cmp_.grad.float().cpu(), ref[2].cpu()) < 1e-2
+    assert _rel_err(snk.grad.cpu(), ref[3].cpu()) < 1e-4
