@@ -16,15 +16,14 @@
 // One workgroup (4 waves) per (token, 16-head group, KV split). With few
 // tokens the token's key slots are split over several workgroups (as in the
 // forward), which then add their dq shares atomically. Thread (h, part) keeps
-// q, dO of head h for channel part `part` (D / 16 channels) in registers and
-// accumulates that part of dq. Rows stream through LDS in chunks of 16: each
+// q, dO of head h for channel part `part` (D / 16 channels) in registers.
+// Rows stream through LDS in chunks of 16: each
 // thread's partial q.k and dO.v sums are summed over the head's 16 lanes
 // (DPP row permutes), lane `part` computes row `part`'s P and dS and shares
-// them through LDS; then every thread adds dS k to its dq part, and the
-// chunk's dkv rows (sums over the 16 heads) come from 16x16x16 MFMAs
-// (dS . Q + P . dO per 16-channel tile) and are added to the fp32 gradient
-// cache rows with atomics. The scores and dq stay on the VALU (dot2 / FMA);
-// the forward's MFMA layouts are the way to move them too.
+// them through LDS. dq (dS . K, accumulated across chunks in registers) and
+// the chunk's dkv rows (dS^T . Q + P^T . dO, sums over the 16 heads, added to
+// the fp32 gradient cache rows with atomics) are 16x16x16 MFMAs per 16-channel
+// tile; the scores stay on the VALU (dot2).
 
 #include <type_traits>
 
@@ -98,7 +97,6 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
   const int h = tid >> 4, part = tid & 15;
   const int hq = k.hg * 16 + h;
   const int t = k.t;
-  float* dqp = bp.dq + ((size_t)t * p.H + hq) * D + part * CP;
   if (k.padded) {   // dq stays zero (the caller zeroes it)
     return;
   }
@@ -113,7 +111,6 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
                                                          ((size_t)t * p.H + hq) * kDV);
   constexpr int CP2 = CP / 2;
   uint32_t qr[CP2], dr[CP2];
-  float dq[CP];
   float dpart = 0.f;
 #pragma unroll
   for (int i = 0; i < CP2; ++i) {
@@ -122,8 +119,13 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
     dr[i] = 2 * c2 < kDV ? dog[c2] : 0u;
     if (2 * c2 < kDV) dpart = dot2<QT>(dr[i], og[c2], dpart);
   }
+  // dq by MFMA: wave w owns 16-channel tiles w, w + 4, ...; lane (g4, c16)
+  // holds heads 4 g4 .. 4 g4 + 3 of channel 16 ct + c16
+  constexpr int NDT = (D / 16 + 3) / 4;
+  const int c16 = lane & 15, g4 = lane >> 4;
+  f32x4 dqt[NDT];
 #pragma unroll
-  for (int i = 0; i < CP; ++i) dq[i] = 0.f;
+  for (int j = 0; j < NDT; ++j) dqt[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float delta = sum16(dpart);
   const float lse2 = p.lse[(size_t)t * p.H + hq] * kLog2e;
   if (part == 0 && k.sp == 0) {
@@ -185,15 +187,27 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
     lds_pd[part][h][0] = pr;
     lds_pd[part][h][1] = dsr;
     __syncthreads();
-    // dq part += sum_r scale dS_r k_r
-    for (int r = 0; r < nr; ++r) {
-      const float w = lds_pd[r][h][1];
-      const uint2* kr = reinterpret_cast<const uint2*>(lds_k + r * KS + part * CP * 2);
+    // col4(base, stride, ch): the 16-bit values of rows 4 g4 .. 4 g4 + 3 at
+    // channel ch, packed as an MFMA operand (rows padded by 16 bytes, so the
+    // four row groups of a read hit distinct banks)
+    auto col4 = [&](const uint8_t* base, int stride, int ch) {
+      const uint32_t v0 = *reinterpret_cast<const uint16_t*>(base + (4 * g4) * stride + ch * 2);
+      const uint32_t v1 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 1) * stride + ch * 2);
+      const uint32_t v2 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 2) * stride + ch * 2);
+      const uint32_t v3 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 3) * stride + ch * 2);
+      return make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+    };
+    // dq[head][ch] += dS[head][key] . K[key][ch]: A = keys 4 g4 .. + 3 of
+    // head c16 (dS rounded to the query dtype), B = the same keys of channel
+    // 16 ct + c16 from the row tile (rows past nr carry dS = 0)
+    {
+      uint2 a_dq;
+      a_dq.x = pack2<QT>(lds_pd[4 * g4][c16][1], lds_pd[4 * g4 + 1][c16][1]);
+      a_dq.y = pack2<QT>(lds_pd[4 * g4 + 2][c16][1], lds_pd[4 * g4 + 3][c16][1]);
 #pragma unroll
-      for (int i = 0; i < CP / 4; ++i) {
-        const uint2 u = kr[i];
-        const float2 a = unpack2<QT>(u.x), b = unpack2<QT>(u.y);
-        dq[4 * i] += w * a.x; dq[4 * i + 1] += w * a.y; dq[4 * i + 2] += w * b.x; dq[4 * i + 3] += w * b.y;
+      for (int j = 0; j < NDT; ++j) {
+        const int ct = wave + 4 * j;
+        if (ct < D / 16) dqt[j] = mfma16k<QT>(a_dq, col4(lds_k, KS, ct * 16 + c16), dqt[j]);
       }
     }
     // dkv rows of the chunk by 16x16x16 MFMA: per 16-channel tile ct,
@@ -205,7 +219,6 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
     // 4g .. 4g + 3 of channel 16 ct + c16 and adds them to the rows' fp32
     // gradients (64-byte runs per key).
     {
-      const int c16 = lane & 15, g4 = lane >> 4;
       uint2 a_ds, a_p;
       a_ds.x = pack2<QT>(lds_pd[c16][4 * g4][1], lds_pd[c16][4 * g4 + 1][1]);
       a_ds.y = pack2<QT>(lds_pd[c16][4 * g4 + 2][1], lds_pd[c16][4 * g4 + 3][1]);
@@ -220,13 +233,6 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
                                                  : bp.d_cmp + (a - cmp_lo) / (D * 2) * D)
                            : nullptr;
       }
-      auto col4 = [&](const uint8_t* base, int stride, int ch) {
-        const uint32_t v0 = *reinterpret_cast<const uint16_t*>(base + (4 * g4) * stride + ch * 2);
-        const uint32_t v1 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 1) * stride + ch * 2);
-        const uint32_t v2 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 2) * stride + ch * 2);
-        const uint32_t v3 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 3) * stride + ch * 2);
-        return make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
-      };
       for (int ct = wave; ct < D / 16; ct += 4) {
         const int ch = ct * 16 + c16;
         f32x4 acc = mfma16k<QT>(a_ds, col4(lds_q, QS, ch), f32x4{0.f, 0.f, 0.f, 0.f});
@@ -238,13 +244,17 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
     }
     __syncthreads();
   }
-  // one split: the workgroup owns the head's dq; several: each adds its share
-  if (p.nsplit == 1) {
+  // one split: the workgroup owns its heads' dq; several: each adds its share
+  float* dqb = bp.dq + ((size_t)t * p.H + k.hg * 16 + 4 * g4) * D + c16;
 #pragma unroll
-    for (int i = 0; i < CP; ++i) dqp[i] = dq[i];
-  } else {
+  for (int j = 0; j < NDT; ++j) {
+    const int ct = wave + 4 * j;
+    if (ct >= D / 16) break;
 #pragma unroll
-    for (int i = 0; i < CP; ++i) atomicAdd(dqp + i, dq[i]);
+    for (int i = 0; i < 4; ++i) {
+      if (p.nsplit == 1) dqb[(size_t)i * D + ct * 16] = dqt[j][i];
+      else atomicAdd(dqb + (size_t)i * D + ct * 16, dqt[j][i]);
+    }
   }
 }
 
