@@ -13,7 +13,9 @@
 //   dkv_j += scale dS_j q  +  [P_j dO, 0]   (summed over heads and tokens)
 //   dsink += -P_sink Delta                   (the sink's value row is zero)
 //
-// One workgroup (4 waves) per (token, 16-head group, KV split). With few
+// One workgroup per (token, head group, KV split): 32 heads (8 waves, two
+// 16-head groups sharing the row tile) when H is a multiple of 32, else 16
+// heads (4 waves). With few
 // tokens the token's key slots are split over several workgroups (as in the
 // forward), which then add their dq shares atomically. Thread (h, part) keeps
 // q, dO of head h for channel part `part` (D / 16 channels) in registers.
@@ -77,16 +79,21 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
-template <int D, typename QT>
-__global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
+// NG 16-head groups per workgroup (1 or 2; 4 NG waves): the groups share
+// the row tile and their dkv contributions are summed (chained MFMAs) before
+// one set of atomics, so NG = 2 halves the row-gradient atomics.
+template <int D, typename QT, int NG>
+__global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
+  constexpr int NT = 256 * NG;                 // threads
+  constexpr int NHD = 16 * NG;                 // heads per workgroup
   constexpr int CP = D / 16;                   // channels per part
   constexpr int CH = D / 8;                    // 16-byte chunks per row
   constexpr int KS = D * 2 + 16;               // LDS row stride (bytes)
-  __shared__ __attribute__((aligned(16))) uint8_t lds_k[kBwdRows * KS];
   constexpr int QS = D * 2 + 16, OS = kDV * 2 + 16;   // padded q / dO row strides (bytes)
-  __shared__ __attribute__((aligned(16))) uint8_t lds_q[16 * QS];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_do[16 * OS];
-  __shared__ float lds_pd[kBwdRows][16][2];    // (P, scale dS) per row and head
+  __shared__ __attribute__((aligned(16))) uint8_t lds_k[kBwdRows * KS];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_q[NHD * QS];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_do[NHD * OS];
+  __shared__ float lds_pd[kBwdRows][NHD][2];   // (P, scale dS) per row and head
 
   const FwdParams& p = bp.f;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -94,8 +101,10 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
   if (item < 0) return;
   Tok k = item_of(p, item);
   resolve<256, D * 2>(p, k, tid, lane, wave, [] {});
-  const int h = tid >> 4, part = tid & 15;
-  const int hq = k.hg * 16 + h;
+  const int hgw = wave >> 2, wl = wave & 3;    // head group in the workgroup, wave in the group
+  const int h = (tid & 255) >> 4, part = tid & 15;
+  const int hw = hgw * 16 + h;                 // head in the workgroup
+  const int hq = k.hg * NHD + hw;
   const int t = k.t;
   if (k.padded) {   // dq stays zero (the caller zeroes it)
     return;
@@ -119,8 +128,9 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
     dr[i] = 2 * c2 < kDV ? dog[c2] : 0u;
     if (2 * c2 < kDV) dpart = dot2<QT>(dr[i], og[c2], dpart);
   }
-  // dq by MFMA: wave w owns 16-channel tiles w, w + 4, ...; lane (g4, c16)
-  // holds heads 4 g4 .. 4 g4 + 3 of channel 16 ct + c16
+  // dq by MFMA: wave wl of head group hgw owns 16-channel tiles wl, wl + 4,
+  // ...; lane (g4, c16) holds the group's heads 4 g4 .. 4 g4 + 3 of channel
+  // 16 ct + c16
   constexpr int NDT = (D / 16 + 3) / 4;
   const int c16 = lane & 15, g4 = lane >> 4;
   f32x4 dqt[NDT];
@@ -134,22 +144,32 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
   }
   {
     const uint4* qs = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.q) +
-                                                     ((size_t)t * p.H + k.hg * 16) * D);
+                                                     ((size_t)t * p.H + k.hg * NHD) * D);
     const uint4* ds = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(bp.dout) +
-                                                     ((size_t)t * p.H + k.hg * 16) * kDV);
-    for (int i = tid; i < 16 * D / 8; i += 256)
+                                                     ((size_t)t * p.H + k.hg * NHD) * kDV);
+    for (int i = tid; i < NHD * D / 8; i += NT)
       *reinterpret_cast<uint4*>(lds_q + (i / (D / 8)) * QS + (i % (D / 8)) * 16) = qs[i];
-    for (int i = tid; i < 16 * kDV / 8; i += 256)
+    for (int i = tid; i < NHD * kDV / 8; i += NT)
       *reinterpret_cast<uint4*>(lds_do + (i / (kDV / 8)) * OS + (i % (kDV / 8)) * 16) = ds[i];
   }
   const float scale = p.scale_log2 / kLog2e;
   const uint64_t ori_lo = reinterpret_cast<uint64_t>(p.ori_kv);
   const uint64_t ori_n = (uint64_t)p.ori_nblocks * p.ori_bs * (D * 2);
   const uint64_t cmp_lo = reinterpret_cast<uint64_t>(p.cmp_kv);
+  // col4(base, stride, ch): the 16-bit values of rows 4 g4 .. 4 g4 + 3 of
+  // `base` at channel ch, packed as an MFMA operand (rows padded by 16 bytes,
+  // so the four row groups of a read hit distinct banks)
+  auto col4 = [&](const uint8_t* base, int stride, int ch) {
+    const uint32_t v0 = *reinterpret_cast<const uint16_t*>(base + (4 * g4) * stride + ch * 2);
+    const uint32_t v1 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 1) * stride + ch * 2);
+    const uint32_t v2 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 2) * stride + ch * 2);
+    const uint32_t v3 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 3) * stride + ch * 2);
+    return make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+  };
 
   for (int c0 = 0; c0 < k.nvalid; c0 += kBwdRows) {
     const int nr = min(kBwdRows, k.nvalid - c0);
-    for (int i = tid; i < kBwdRows * CH; i += 256) {
+    for (int i = tid; i < kBwdRows * CH; i += NT) {
       const int r = i / CH, c = i - r * CH;
       const uint64_t a = lds_rows[c0 + min(r, nr - 1)];
       *reinterpret_cast<uint4*>(lds_k + r * KS + c * 16) = *reinterpret_cast<const uint4*>(a + c * 16);
@@ -184,46 +204,40 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
       pr = __builtin_amdgcn_exp2f(s_row * p.scale_log2 - lse2);
       dsr = pr * (dp_row - delta) * scale;
     }
-    lds_pd[part][h][0] = pr;
-    lds_pd[part][h][1] = dsr;
+    lds_pd[part][hw][0] = pr;
+    lds_pd[part][hw][1] = dsr;
     __syncthreads();
-    // col4(base, stride, ch): the 16-bit values of rows 4 g4 .. 4 g4 + 3 at
-    // channel ch, packed as an MFMA operand (rows padded by 16 bytes, so the
-    // four row groups of a read hit distinct banks)
-    auto col4 = [&](const uint8_t* base, int stride, int ch) {
-      const uint32_t v0 = *reinterpret_cast<const uint16_t*>(base + (4 * g4) * stride + ch * 2);
-      const uint32_t v1 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 1) * stride + ch * 2);
-      const uint32_t v2 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 2) * stride + ch * 2);
-      const uint32_t v3 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 3) * stride + ch * 2);
-      return make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
-    };
-    // dq[head][ch] += dS[head][key] . K[key][ch]: A = keys 4 g4 .. + 3 of
-    // head c16 (dS rounded to the query dtype), B = the same keys of channel
-    // 16 ct + c16 from the row tile (rows past nr carry dS = 0)
+    // dq[head][ch] += dS[head][key] . K[key][ch]: A = keys 4 g4 .. + 3 of the
+    // group's head c16 (dS rounded to the query dtype), B = the same keys of
+    // channel 16 ct + c16 from the row tile (rows past nr carry dS = 0)
     {
       uint2 a_dq;
-      a_dq.x = pack2<QT>(lds_pd[4 * g4][c16][1], lds_pd[4 * g4 + 1][c16][1]);
-      a_dq.y = pack2<QT>(lds_pd[4 * g4 + 2][c16][1], lds_pd[4 * g4 + 3][c16][1]);
+      a_dq.x = pack2<QT>(lds_pd[4 * g4][hgw * 16 + c16][1], lds_pd[4 * g4 + 1][hgw * 16 + c16][1]);
+      a_dq.y = pack2<QT>(lds_pd[4 * g4 + 2][hgw * 16 + c16][1], lds_pd[4 * g4 + 3][hgw * 16 + c16][1]);
 #pragma unroll
       for (int j = 0; j < NDT; ++j) {
-        const int ct = wave + 4 * j;
+        const int ct = wl + 4 * j;
         if (ct < D / 16) dqt[j] = mfma16k<QT>(a_dq, col4(lds_k, KS, ct * 16 + c16), dqt[j]);
       }
     }
-    // dkv rows of the chunk by 16x16x16 MFMA: per 16-channel tile ct,
-    // dK[key][ch] = dS[key][head] . Q[head][ch] (+ P[key][head] . dO[head][ch]
-    // for ch < 512). A = 4 heads (4g .. 4g + 3) of key c16 from the (P, dS)
-    // table, rounded to the query dtype; B = the same 4 heads of channel
-    // 16 ct + c16 from the q / dO tiles (rows padded so the four head-row
-    // groups of a read hit distinct banks). Lane (g, c16) then holds keys
-    // 4g .. 4g + 3 of channel 16 ct + c16 and adds them to the rows' fp32
-    // gradients (64-byte runs per key).
+    // dkv rows of the chunk by 16x16x16 MFMA: per 16-channel tile ct (wave
+    // w takes tiles w, w + 4 NG, ...), dK[key][ch] = sum over the head
+    // groups of dS[key][head] . Q[head][ch] (+ P[key][head] . dO[head][ch]
+    // for ch < 512), one chained MFMA per group. A = 4 heads (4 g4 .. + 3)
+    // of key c16 from the (P, dS) table, rounded to the query dtype; B = the
+    // same 4 heads of channel 16 ct + c16 from the q / dO tiles. Lane (g4,
+    // c16) then holds keys 4 g4 .. + 3 of channel 16 ct + c16 and adds them
+    // to the rows' fp32 gradients (64-byte runs per key).
     {
-      uint2 a_ds, a_p;
-      a_ds.x = pack2<QT>(lds_pd[c16][4 * g4][1], lds_pd[c16][4 * g4 + 1][1]);
-      a_ds.y = pack2<QT>(lds_pd[c16][4 * g4 + 2][1], lds_pd[c16][4 * g4 + 3][1]);
-      a_p.x = pack2<QT>(lds_pd[c16][4 * g4][0], lds_pd[c16][4 * g4 + 1][0]);
-      a_p.y = pack2<QT>(lds_pd[c16][4 * g4 + 2][0], lds_pd[c16][4 * g4 + 3][0]);
+      uint2 a_ds[NG], a_p[NG];
+#pragma unroll
+      for (int gg = 0; gg < NG; ++gg) {
+        const int hb = gg * 16 + 4 * g4;
+        a_ds[gg].x = pack2<QT>(lds_pd[c16][hb][1], lds_pd[c16][hb + 1][1]);
+        a_ds[gg].y = pack2<QT>(lds_pd[c16][hb + 2][1], lds_pd[c16][hb + 3][1]);
+        a_p[gg].x = pack2<QT>(lds_pd[c16][hb][0], lds_pd[c16][hb + 1][0]);
+        a_p[gg].y = pack2<QT>(lds_pd[c16][hb + 2][0], lds_pd[c16][hb + 3][0]);
+      }
       float* grow[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -233,10 +247,14 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
                                                  : bp.d_cmp + (a - cmp_lo) / (D * 2) * D)
                            : nullptr;
       }
-      for (int ct = wave; ct < D / 16; ct += 4) {
+      for (int ct = wave; ct < D / 16; ct += 4 * NG) {
         const int ch = ct * 16 + c16;
-        f32x4 acc = mfma16k<QT>(a_ds, col4(lds_q, QS, ch), f32x4{0.f, 0.f, 0.f, 0.f});
-        if (ct < kDV / 16) acc = mfma16k<QT>(a_p, col4(lds_do, OS, ch), acc);
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int gg = 0; gg < NG; ++gg) {
+          acc = mfma16k<QT>(a_ds[gg], col4(lds_q + gg * 16 * QS, QS, ch), acc);
+          if (ct < kDV / 16) acc = mfma16k<QT>(a_p[gg], col4(lds_do + gg * 16 * OS, OS, ch), acc);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           if (grow[i]) atomicAdd(grow[i] + ch, acc[i]);
@@ -245,10 +263,10 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
     __syncthreads();
   }
   // one split: the workgroup owns its heads' dq; several: each adds its share
-  float* dqb = bp.dq + ((size_t)t * p.H + k.hg * 16 + 4 * g4) * D + c16;
+  float* dqb = bp.dq + ((size_t)t * p.H + k.hg * NHD + hgw * 16 + 4 * g4) * D + c16;
 #pragma unroll
   for (int j = 0; j < NDT; ++j) {
-    const int ct = wave + 4 * j;
+    const int ct = wl + 4 * j;
     if (ct >= D / 16) break;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -258,12 +276,17 @@ __global__ void __launch_bounds__(256) sas_bwd_kernel(const BwdParams bp) {
   }
 }
 
-template <int D, typename QT>
+template <int D, typename QT, int NG>
 int launch_bwd(const BwdParams& bp, int nblocks, hipStream_t st) {
-  hipLaunchKernelGGL((sas_bwd_kernel<D, QT>), dim3(nblocks), dim3(256), 0, st, bp);
+  hipLaunchKernelGGL((sas_bwd_kernel<D, QT, NG>), dim3(nblocks), dim3(256 * NG), 0, st, bp);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(SAS_ELAUNCH, "sas_bwd launch: %s", hipGetErrorString(e));
   return SAS_OK;
+}
+
+template <int D, typename QT>
+int launch_bwd_ng(const BwdParams& bp, int ng, int nblocks, hipStream_t st) {
+  return ng == 2 ? launch_bwd<D, QT, 2>(bp, nblocks, st) : launch_bwd<D, QT, 1>(bp, nblocks, st);
 }
 
 }  // namespace
@@ -323,11 +346,14 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   fp.scale_log2 = a->softmax_scale * kLog2e;
   // KV splits: the caller's count, else enough (token, head group, split)
   // workgroups for two per CU, each split at least 64 slots
-  fp.nhg = (int)a->H / 16;
+  // two 16-head groups per workgroup when H allows (half the dkv atomics)
+  const int ng = a->H % 32 == 0 ? 2 : 1;
+  fp.nhg = (int)a->H / (16 * ng);
   int ns = a->num_splits;
   if (ns <= 0) {
+    // enough (token, head groups, split) workgroups for 8 waves per CU
     const long long items = a->T * fp.nhg;
-    const long long want = (2 * kCus + items - 1) / items;
+    const long long want = (2 * kCus / ng + items - 1) / items;
     ns = (int)std::min<long long>(want, (nslots + 63) / 64);
   }
   ns = std::max(1, std::min(ns, 64));
@@ -343,6 +369,8 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   const int nblocks = (int)((a->T + kXcds - 1) / kXcds) * fp.nhg * fp.nsplit * kXcds;
   hipStream_t st = (hipStream_t)stream;
   if (a->q_dtype == SAS_DT_BF16)
-    return a->D == 576 ? launch_bwd<576, __bf16>(bp, nblocks, st) : launch_bwd<512, __bf16>(bp, nblocks, st);
-  return a->D == 576 ? launch_bwd<576, _Float16>(bp, nblocks, st) : launch_bwd<512, _Float16>(bp, nblocks, st);
+    return a->D == 576 ? launch_bwd_ng<576, __bf16>(bp, ng, nblocks, st)
+                       : launch_bwd_ng<512, __bf16>(bp, ng, nblocks, st);
+  return a->D == 576 ? launch_bwd_ng<576, _Float16>(bp, ng, nblocks, st)
+                     : launch_bwd_ng<512, _Float16>(bp, ng, nblocks, st);
 }
