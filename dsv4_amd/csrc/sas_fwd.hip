@@ -1090,11 +1090,12 @@ sas_dec_kernel(const FwdParams p) {
 constexpr int kCombineThreads = 256;
 constexpr int kMaxCombineSplits = 64;
 
-// One workgroup per (token, 2 heads), thread = (head, 4 channels).
+// One workgroup per (token, 4 heads), thread = (head, 8 channels): 16-byte
+// fp16 partial loads (C2 call 19.95 -> 19.7 us against 4 channels).
 template <typename QT>
 __global__ void __launch_bounds__(kCombineThreads)
 sas_combine_kernel(const FwdParams p) {
-  constexpr int kHeads = kCombineThreads / (kDV / 4);  // 2
+  constexpr int kHeads = kCombineThreads / (kDV / kCombineCpt);   // heads per workgroup
   const int nhb = (p.H + kHeads - 1) / kHeads;
   // token t's workgroups go to the XCD its split workgroups ran on
   // (item_index's dealing), whose L2 still holds the partials they wrote
@@ -1209,7 +1210,7 @@ int dispatch_hw(int hw, int nw, const FwdParams& fp, int nb, hipStream_t st) {
 }
 
 int launch_combine(const FwdParams& fp, int out_dtype, hipStream_t st) {
-  constexpr int kHeads = kCombineThreads / (kDV / 4);
+  constexpr int kHeads = kCombineThreads / (kDV / kCombineCpt);
   const dim3 grid((unsigned)(((fp.T + kXcds - 1) / kXcds) * kXcds * ((fp.H + kHeads - 1) / kHeads)));
   if (out_dtype == SAS_DT_BF16)
     hipLaunchKernelGGL(sas_combine_kernel<__bf16>, grid, dim3(kCombineThreads), 0, st, fp);

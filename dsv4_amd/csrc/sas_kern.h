@@ -205,14 +205,6 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
-template <typename QT>
-__device__ __forceinline__ void store_out4(const FwdParams& p, int t, int h, int c4, float4 o, float inv) {
-  const uint32_t w0 = pack2<QT>(o.x * inv, o.y * inv);
-  const uint32_t w1 = pack2<QT>(o.z * inv, o.w * inv);
-  *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + ((size_t)t * p.H + h) * kDV + c4 * 4) =
-      make_uint2(w0, w1);
-}
-
 // Split-partial O element type: fp16 under bf16 outputs (scaled by a power
 // of two per 256-channel half, 8x finer than the output's rounding), fp32
 // under fp16 outputs (fp16 would round as coarsely as the output does).
@@ -220,36 +212,45 @@ template <typename QT> struct PartSel { using T = _Float16; };
 template <> struct PartSel<_Float16> { using T = float; };
 template <typename QT> using PartT = typename PartSel<QT>::T;
 
+// Channels per combine thread (4: 8-byte fp16 partial loads, 8: 16-byte)
+#ifndef SAS_COMBINE_CPT
+#define SAS_COMBINE_CPT 8
+#endif
+constexpr int kCombineCpt = SAS_COMBINE_CPT;
+
 // Merge the nsplit partials of (token t, heads [h0, h0 + nh)) with the sink
 // into out / lse: M = max(sink, m_i), L = 2^(sink-M) + sum_i l_i 2^(m_i-M),
 // out = sum_i 2^(m_i-M) O_i / L, lse = (M ln 2) + ln L (a running merge over
-// i, kB splits' loads in flight together). Partial O_i is stored as fp16
-// values O_i 2^e_i (PartT: fp16, or fp32 with e_i = 0) with one exponent e_i
-// per 256-channel half, so it is recovered exactly as ldexp(value, -e_i). A negative l marks a padded token
-// (out = 0, lse = 0).
+// i, kB splits' loads in flight together). Partial O_i is stored as values
+// O_i 2^e_i (PartT: fp16, or fp32 with e_i = 0) with one exponent e_i per
+// 256-channel half, so it is recovered exactly as ldexp(value, -e_i). A
+// thread owns kCombineCpt consecutive channels of one head. A negative l
+// marks a padded token (out = 0, lse = 0).
 template <typename QT>
 __device__ __forceinline__ void merge_partials(const FwdParams& p, int t, int h0, int nh, int tid,
                                                int nthreads) {
-  constexpr int kB = 4;
+  constexpr int kB = 4, CPT = kCombineCpt, NG = kDV / CPT;   // channel groups per head
   const int S = p.nsplit;
   using PT = PartT<QT>;
-  typedef PT v4 __attribute__((ext_vector_type(4)));
-  const v4* po = reinterpret_cast<const v4*>(p.part_o) + (size_t)t * S * p.H * (kDV / 4);
+  typedef PT vc __attribute__((ext_vector_type(CPT)));
+  const vc* po = reinterpret_cast<const vc*>(p.part_o) + (size_t)t * S * p.H * NG;
   const float* pm = p.part_ml + (size_t)t * S * p.H * 4;
-  for (int e = tid; e < nh * (kDV / 4); e += nthreads) {
-    const int h = h0 + e / (kDV / 4), c4 = e % (kDV / 4);
-    const int half = c4 >= kDV / 8;
+  for (int e = tid; e < nh * NG; e += nthreads) {
+    const int h = h0 + e / NG, cg = e % NG;
+    const int half = cg >= NG / 2;
     float M = p.sinks[h] * kLog2e, L = 1.f;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    float o[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) o[c] = 0.f;
     bool pad = false;
     for (int s0 = 0; s0 < S; s0 += kB) {
       float4 ml[kB];
-      v4 v[kB];
+      vc v[kB];
 #pragma unroll
       for (int j = 0; j < kB; ++j) {
         const size_t row = (size_t)min(s0 + j, S - 1) * p.H + h;
         ml[j] = *reinterpret_cast<const float4*>(pm + row * 4);
-        v[j] = po[row * (kDV / 4) + c4];
+        v[j] = po[row * NG + cg];
       }
 #pragma unroll
       for (int j = 0; j < kB; ++j) {
@@ -257,19 +258,26 @@ __device__ __forceinline__ void merge_partials(const FwdParams& p, int t, int h0
         pad |= ml[j].y < 0.f;
         if (ml[j].x > M) {
           const float a = exp2f(M - ml[j].x);
-          L *= a; o.x *= a; o.y *= a; o.z *= a; o.w *= a;
+          L *= a;
+#pragma unroll
+          for (int c = 0; c < CPT; ++c) o[c] *= a;
           M = ml[j].x;
         }
         const float w = ml[j].x == -INFINITY ? 0.f : exp2f(ml[j].x - M);
         const int ne = -(int)(half ? ml[j].w : ml[j].z);
-        const v4 x = v[j];
         L += w * ml[j].y;
-        o.x += ldexpf(w * (float)x[0], ne); o.y += ldexpf(w * (float)x[1], ne);
-        o.z += ldexpf(w * (float)x[2], ne); o.w += ldexpf(w * (float)x[3], ne);
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) o[c] += ldexpf(w * (float)v[j][c], ne);
       }
     }
-    store_out4<QT>(p, t, h, c4, o, pad ? 0.f : 1.f / L);
-    if (c4 == 0) p.lse[(size_t)t * p.H + h] = pad ? 0.f : M * kLn2 + logf(L);
+    const float inv = pad ? 0.f : 1.f / L;
+    uint32_t w[CPT / 2];
+#pragma unroll
+    for (int c = 0; c < CPT / 2; ++c) w[c] = pack2<QT>(o[2 * c] * inv, o[2 * c + 1] * inv);
+    uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + ((size_t)t * p.H + h) * kDV + cg * CPT;
+    if constexpr (CPT == 8) *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+    else *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+    if (cg == 0) p.lse[(size_t)t * p.H + h] = pad ? 0.f : M * kLn2 + logf(L);
   }
 }
 
