@@ -341,6 +341,12 @@ EDGE = {
     # and 64-head groups (600 query rows)
     "d512": dict(B=2, H=64, q_lens=[3, 2], kv_lens=[2500, 800], K=100, D=512),
     "d512_prefill": dict(B=1, H=64, q_lens=[600], kv_lens=[2400], K=128, D=512),
+    # window of one row (win_left 0) and of 256 rows
+    "win0": dict(B=2, H=32, q_lens=[3, 1], kv_lens=[500, 90], K=64, win=0),
+    "win255_prefill": dict(B=1, H=64, q_lens=[300], kv_lens=[1200], K=96, win=255),
+    # block size 128, an odd top-k width, H = 128 in fp16
+    "bs128_k77": dict(B=3, H=64, q_lens=[1, 2, 1], kv_lens=[3000, 777, 129], K=77, bs=128),
+    "h128_fp16": dict(B=2, H=128, q_lens=[2, 1], kv_lens=[2500, 1000], K=256, dtype=torch.float16),
 }
 
 
