@@ -15,17 +15,17 @@
 //
 // One workgroup per (token, head group, KV split): 32 heads (8 waves, two
 // 16-head groups sharing the row tile) when H is a multiple of 32, else 16
-// heads (4 waves). With few
-// tokens the token's key slots are split over several workgroups (as in the
-// forward), which then add their dq shares atomically. Thread (h, part) keeps
-// q, dO of head h for channel part `part` (D / 16 channels) in registers.
-// Rows stream through LDS in chunks of 16: each
-// thread's partial q.k and dO.v sums are summed over the head's 16 lanes
-// (DPP row permutes), lane `part` computes row `part`'s P and dS and shares
-// them through LDS. dq (dS . K, accumulated across chunks in registers) and
-// the chunk's dkv rows (dS^T . Q + P^T . dO, sums over the 16 heads, added to
-// the fp32 gradient cache rows with atomics) are 16x16x16 MFMAs per 16-channel
-// tile; the scores stay on the VALU (dot2).
+// heads (4 waves). With few tokens the token's key slots are split over
+// several workgroups (as in the forward), which then add their dq shares
+// atomically. Thread (h, part) sums Delta = dO . O over D / 16 channels of
+// head h (16 lanes, DPP sums). Rows
+// stream through LDS in chunks of 16 (the next chunk's loads in flight in
+// registers): S^T and dP^T are 16x16x32 MFMAs (each head group's four waves
+// take a quarter of the k-steps and add the partial tiles through LDS), P
+// and dS go to an LDS table, then dq (dS . K, accumulated across chunks in
+// registers) and the chunk's dkv rows (dS^T . Q + P^T . dO, summed over the
+// heads, added to the fp32 gradient cache rows with atomics) are 16x16x16
+// MFMAs per 16-channel tile.
 
 #include <type_traits>
 
@@ -94,6 +94,8 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_q[NHD * QS];
   __shared__ __attribute__((aligned(16))) uint8_t lds_do[NHD * OS];
   __shared__ float lds_pd[kBwdRows][NHD][2];   // (P, scale dS) per row and head
+  __shared__ f32x4 lds_red[4 * NG][2][64];      // per wave: partial S^T and dP^T tiles
+  __shared__ float lds_hd[NHD][2];              // per head: Delta, lse (log2 units)
 
   const FwdParams& p = bp.f;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -112,21 +114,16 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
 
   // this thread's q / dO channels as packed pairs (dO zero past channel
   // 512), Delta = dO . O over the head's 16 lanes
-  const uint32_t* qg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(p.q) +
-                                                         ((size_t)t * p.H + hq) * D + part * CP);
   const uint32_t* dog = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(bp.dout) +
                                                           ((size_t)t * p.H + hq) * kDV);
   const uint32_t* og = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(bp.out) +
                                                          ((size_t)t * p.H + hq) * kDV);
   constexpr int CP2 = CP / 2;
-  uint32_t qr[CP2], dr[CP2];
   float dpart = 0.f;
 #pragma unroll
   for (int i = 0; i < CP2; ++i) {
     const int c2 = part * CP2 + i;   // channel pair
-    qr[i] = qg[i];
-    dr[i] = 2 * c2 < kDV ? dog[c2] : 0u;
-    if (2 * c2 < kDV) dpart = dot2<QT>(dr[i], og[c2], dpart);
+    if (2 * c2 < kDV) dpart = dot2<QT>(dog[c2], og[c2], dpart);
   }
   // dq by MFMA: wave wl of head group hgw owns 16-channel tiles wl, wl + 4,
   // ...; lane (g4, c16) holds the group's heads 4 g4 .. 4 g4 + 3 of channel
@@ -138,6 +135,7 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
   for (int j = 0; j < NDT; ++j) dqt[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float delta = sum16(dpart);
   const float lse2 = p.lse[(size_t)t * p.H + hq] * kLog2e;
+  if (part == 0) { lds_hd[hw][0] = delta; lds_hd[hw][1] = lse2; }
   if (part == 0 && k.sp == 0) {
     const float psink = __builtin_amdgcn_exp2f(p.sinks[hq] * kLog2e - lse2);
     atomicAdd(bp.d_sinks + hq, -psink * delta);
@@ -167,45 +165,78 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
     return make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
   };
 
+  // Row chunks are double-buffered through registers: the loads of chunk
+  // c + 1 are issued right after chunk c is in LDS and land during its
+  // compute (rows past the end repeat the last row: their P and dS are 0).
+  constexpr int NLD = (kBwdRows * CH + NT - 1) / NT;
+  uint4 rbuf[NLD];
+  auto load_rows = [&](int c0n) {
+    const int nrn = min(kBwdRows, k.nvalid - c0n);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      const int i = tid + NT * j;
+      if (i < kBwdRows * CH) {
+        const int r = i / CH, c = i - r * CH;
+        const uint64_t a = lds_rows[c0n + min(r, nrn - 1)];
+        rbuf[j] = *reinterpret_cast<const uint4*>(a + c * 16);
+      }
+    }
+  };
+  if (k.nvalid > 0) load_rows(0);
+
   for (int c0 = 0; c0 < k.nvalid; c0 += kBwdRows) {
     const int nr = min(kBwdRows, k.nvalid - c0);
-    for (int i = tid; i < kBwdRows * CH; i += NT) {
-      const int r = i / CH, c = i - r * CH;
-      const uint64_t a = lds_rows[c0 + min(r, nr - 1)];
-      *reinterpret_cast<uint4*>(lds_k + r * KS + c * 16) = *reinterpret_cast<const uint4*>(a + c * 16);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      const int i = tid + NT * j;
+      if (i < kBwdRows * CH) {
+        const int r = i / CH, c = i - r * CH;
+        *reinterpret_cast<uint4*>(lds_k + r * KS + c * 16) = rbuf[j];
+      }
     }
     __syncthreads();
-    float sv[kBwdRows], dv[kBwdRows];
+    if (c0 + kBwdRows < k.nvalid) load_rows(c0 + kBwdRows);
+    // S^T[key][head] = K . Q^T and dP^T = V . dO^T by 16x16x32 MFMA: the
+    // four waves of head group hgw take k-steps wl, wl + 4, ... (A = 8
+    // channels of key c16 from the row tile, B = the same channels of head
+    // c16 from the q / dO tile) and add their partial tiles through LDS;
+    // lane (g4, c16) then holds keys 4 g4 .. + 3 of head c16.
+    {
+      f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f}, dacc = sacc;
+      const uint8_t* kb = lds_k + c16 * KS + g4 * 16;
+      const uint8_t* qb = lds_q + (hgw * 16 + c16) * QS + g4 * 16;
+      const uint8_t* ob = lds_do + (hgw * 16 + c16) * OS + g4 * 16;
 #pragma unroll
-    for (int r = 0; r < kBwdRows; ++r) {
-      const uint2* kr = reinterpret_cast<const uint2*>(lds_k + r * KS + part * CP * 2);
-      float s = 0.f, d = 0.f;
-#pragma unroll
-      for (int i = 0; i < CP / 4; ++i) {
-        const uint2 w = kr[i];
-        s = dot2<QT>(qr[2 * i], w.x, s);
-        s = dot2<QT>(qr[2 * i + 1], w.y, s);
-        d = dot2<QT>(dr[2 * i], w.x, d);       // dr is zero past channel 512
-        d = dot2<QT>(dr[2 * i + 1], w.y, d);
+      for (int ks = wl; ks < D / 32; ks += 4) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(kb + ks * 64);
+        sacc = mfma32k<QT>(kf, *reinterpret_cast<const uint4*>(qb + ks * 64), sacc);
+        if (ks < kDV / 32) dacc = mfma32k<QT>(kf, *reinterpret_cast<const uint4*>(ob + ks * 64), dacc);
       }
-      sv[r] = s;
-      dv[r] = d;
+      lds_red[wave][0][lane] = sacc;
+      lds_red[wave][1][lane] = dacc;
     }
-    // every lane of the head gets each row's sums; lane `part` keeps row `part`
-    float s_row = 0.f, dp_row = 0.f;
+    __syncthreads();
+    if (wl == 0) {
+      f32x4 sv = lds_red[hgw * 4][0][lane], dv = lds_red[hgw * 4][1][lane];
 #pragma unroll
-    for (int r = 0; r < kBwdRows; ++r) {
-      const float a = sum16(sv[r]), b = sum16(dv[r]);
-      s_row = r == part ? a : s_row;
-      dp_row = r == part ? b : dp_row;
+      for (int w = 1; w < 4; ++w) {
+        sv += lds_red[hgw * 4 + w][0][lane];
+        dv += lds_red[hgw * 4 + w][1][lane];
+      }
+      const int hh = hgw * 16 + c16;
+      const float dl = lds_hd[hh][0], l2 = lds_hd[hh][1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = 4 * g4 + i;
+        float pr = 0.f, dsr = 0.f;
+        if (key < nr) {
+          pr = __builtin_amdgcn_exp2f(sv[i] * p.scale_log2 - l2);
+          dsr = pr * (dv[i] - dl) * scale;
+        }
+        lds_pd[key][hh][0] = pr;
+        lds_pd[key][hh][1] = dsr;
+      }
     }
-    float pr = 0.f, dsr = 0.f;
-    if (part < nr) {
-      pr = __builtin_amdgcn_exp2f(s_row * p.scale_log2 - lse2);
-      dsr = pr * (dp_row - delta) * scale;
-    }
-    lds_pd[part][hw][0] = pr;
-    lds_pd[part][hw][1] = dsr;
     __syncthreads();
     // dq[head][ch] += dS[head][key] . K[key][ch]: A = keys 4 g4 .. + 3 of the
     // group's head c16 (dS rounded to the query dtype), B = the same keys of
