@@ -154,15 +154,14 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
   const uint64_t ori_lo = reinterpret_cast<uint64_t>(p.ori_kv);
   const uint64_t ori_n = (uint64_t)p.ori_nblocks * p.ori_bs * (D * 2);
   const uint64_t cmp_lo = reinterpret_cast<uint64_t>(p.cmp_kv);
-  // col4(base, stride, ch): the 16-bit values of rows 4 g4 .. 4 g4 + 3 of
-  // `base` at channel ch, packed as an MFMA operand (rows padded by 16 bytes,
-  // so the four row groups of a read hit distinct banks)
-  auto col4 = [&](const uint8_t* base, int stride, int ch) {
-    const uint32_t v0 = *reinterpret_cast<const uint16_t*>(base + (4 * g4) * stride + ch * 2);
-    const uint32_t v1 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 1) * stride + ch * 2);
-    const uint32_t v2 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 2) * stride + ch * 2);
-    const uint32_t v3 = *reinterpret_cast<const uint16_t*>(base + (4 * g4 + 3) * stride + ch * 2);
-    return make_uint2(v0 | (v1 << 16), v2 | (v3 << 16));
+  // col4(base, stride, ct): the 16-bit values of rows 4 g4 .. 4 g4 + 3 of
+  // `base` at channel 16 ct + c16, packed as an MFMA operand, by one
+  // transposed read: lane (g4, c16) addresses row 4 g4 + c16 / 4 at channels
+  // 16 ct + 4 (c16 & 3) .. + 3 and receives its channel of the four rows
+  // (rows padded by 16 bytes, so the row groups spread over the banks)
+  auto col4 = [&](const uint8_t* base, int stride, int ct) {
+    const uint8_t* a = base + (4 * g4 + (c16 >> 2)) * stride + (ct * 16 + 4 * (c16 & 3)) * 2;
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a)));
   };
 
   // Row chunks are double-buffered through registers: the loads of chunk
@@ -248,7 +247,7 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
 #pragma unroll
       for (int j = 0; j < NDT; ++j) {
         const int ct = wl + 4 * j;
-        if (ct < D / 16) dqt[j] = mfma16k<QT>(a_dq, col4(lds_k, KS, ct * 16 + c16), dqt[j]);
+        if (ct < D / 16) dqt[j] = mfma16k<QT>(a_dq, col4(lds_k, KS, ct), dqt[j]);
       }
     }
     // dkv rows of the chunk by 16x16x16 MFMA: per 16-channel tile ct (wave
@@ -283,8 +282,8 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int gg = 0; gg < NG; ++gg) {
-          acc = mfma16k<QT>(a_ds[gg], col4(lds_q + gg * 16 * QS, QS, ch), acc);
-          if (ct < kDV / 16) acc = mfma16k<QT>(a_p[gg], col4(lds_do + gg * 16 * OS, OS, ch), acc);
+          acc = mfma16k<QT>(a_ds[gg], col4(lds_q + gg * 16 * QS, QS, ct), acc);
+          if (ct < kDV / 16) acc = mfma16k<QT>(a_p[gg], col4(lds_do + gg * 16 * OS, OS, ct), acc);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
