@@ -221,3 +221,64 @@ def test_gpu_autograd_binding():
     assert _rel_err(ori.grad.float().cpu(), ref[1].cpu()) < 1e-2
     assert _rel_err(cmp_.grad.float().cpu(), ref[2].cpu()) < 1e-2
     assert _rel_err(snk.grad.cpu(), ref[3].cpu()) < 1e-4
+
+
+@pytest.mark.gpu
+def test_gpu_backward_bsnd_padding_matches_tnd():
+    """BSND q [B, S, N, D] with per-batch lengths: the valid rows' dq and the
+    cache / sink gradients equal the TND backward of the same tokens up to
+    summation order (the two layouts get different KV split counts, so bf16
+    dq may differ by a rounding step), and the padded rows' dq is zero."""
+    from tests.test_gpu_parity import _small
+    from dsv4_amd.api import sparse_attn_sharedkv, sparse_attn_sharedkv_backward
+    inp = _small(B=2, H=64, q_lens=[3, 1], kv_lens=[800, 400], K=64)
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    out, lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+    g = torch.Generator().manual_seed(9)
+    dout = torch.randn(out.shape, generator=g).to(out.dtype).cuda()
+    ref = sparse_attn_sharedkv_backward(dout, d.q, out, lse, **kw)
+    slot = [(0, 0), (0, 1), (0, 2), (1, 0)]                       # (b, s) of the 4 packed tokens
+    q_b = torch.zeros(2, 3, 64, 576, dtype=torch.bfloat16, device="cuda")
+    idx_b = torch.full((2, 3, 1, 64), -1, dtype=torch.int32, device="cuda")
+    o_b = torch.zeros(2, 3, 64, 512, dtype=torch.bfloat16, device="cuda")
+    l_b = torch.zeros(2, 3, 64, dtype=torch.float32, device="cuda")
+    do_b = torch.zeros(2, 3, 64, 512, dtype=torch.bfloat16, device="cuda")
+    for t_, (b, s_) in enumerate(slot):
+        q_b[b, s_], idx_b[b, s_], o_b[b, s_], l_b[b, s_], do_b[b, s_] = (
+            d.q[t_], d.cmp_idx[t_], out[t_], lse[t_], dout[t_])
+    kwb = dict(kw, layout_q="BSND", cmp_sparse_indices=idx_b)
+    dq_b, d_ori, d_cmp, d_snk = sparse_attn_sharedkv_backward(do_b, q_b, o_b, l_b, **kwb)
+    torch.cuda.synchronize()
+    assert dq_b.shape == q_b.shape
+    for t_, (b, s_) in enumerate(slot):
+        assert _rel_err(dq_b[b, s_].float().cpu(), ref[0][t_].float().cpu()) < 1e-2
+    assert torch.count_nonzero(dq_b[1, 1:].cpu().float()) == 0
+    assert _rel_err(d_ori.cpu(), ref[1].cpu()) < 1e-4 and _rel_err(d_cmp.cpu(), ref[2].cpu()) < 1e-4
+    assert _rel_err(d_snk.cpu(), ref[3].cpu()) < 1e-4
+
+
+@pytest.mark.gpu
+def test_gpu_backward_h48_d512_matches_oracle():
+    """H = 48 (three 16-head workgroups per token) at D = 512."""
+    from tests.test_gpu_parity import _small
+    from dsv4_amd.api import sparse_attn_sharedkv, sparse_attn_sharedkv_backward
+    inp = _small(B=2, H=48, q_lens=[3, 1], kv_lens=[2000, 700], K=100, D=512)
+    c = inp.cfg
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    out, lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+    g = torch.Generator().manual_seed(10)
+    dout = torch.randn(out.shape, generator=g).to(out.dtype)
+    dq, d_ori, d_cmp, d_snk = sparse_attn_sharedkv_backward(dout.cuda(), d.q, out, lse, **kw)
+    torch.cuda.synchronize()
+    r = BR.backward_paged(inp.q, dout, ori_kv=inp.ori_kv, ori_block_table=inp.ori_bt,
+                          cu_seqlens_q=inp.cu_seqlens_q, seqused_kv=inp.seqused_kv, sinks=inp.sinks,
+                          softmax_scale=c.scale, cmp_kv=inp.cmp_kv, cmp_block_table=inp.cmp_bt,
+                          cmp_sparse_indices=inp.cmp_idx, cmp_ratio=c.cmp_ratio, ori_win_left=c.win_left)
+    assert _rel_err(dq.cpu(), r["dq"]) < 2e-2
+    rows, grads = r["d_ori"]
+    assert _rel_err(d_ori.cpu().reshape(-1, 512)[rows], grads) < 2e-2
+    rows, grads = r["d_cmp"]
+    assert _rel_err(d_cmp.cpu().reshape(-1, 512)[rows], grads) < 2e-2
+    assert _rel_err(d_snk.cpu(), r["d_sinks"]) < 2e-2
