@@ -343,6 +343,21 @@ def main():
     split_gbs = kv_bytes / (us_split * 1e-6) / 1e9
     log(f"C2 split kernel: {us_split:.2f} us/launch ({sp_wall * 1e3 / args.steps:.2f} us wall), "
         f"{split_gbs:.0f} GB/s; combine {us_comb:.2f} us/launch")
+    # the same calls captured once in a HIP graph (16 calls, one per input
+    # rotation) and replayed: what a serving loop that replays captured
+    # launches pays per call
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for c in calls:
+                c.launch(side)
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // len(calls))
+    g_ms, _ = time_launches(lambda i, st: graph.replay(), 1, reps, 2)
+    us_graph = g_ms * 1e3 / (reps * len(calls))
+    log(f"C2 decode in a HIP graph: {us_graph:.2f} us/call")
     # API wall time (host resolution + launch), reported separately
     from dsv4_amd.api import sparse_attn_sharedkv
     kw = inp.api_kwargs()
@@ -438,6 +453,7 @@ def main():
                                "ctx U[8K,32K], paged bs64", "B": 32, "H": 64, "topk": 512,
                    "window": 128, "parallelism": "single GPU"},
         "decode_us_per_call": round(us_call, 3),
+        "decode_us_per_call_graph": round(us_graph, 3),
         "split_kernel_us": round(us_split, 3),
         "combine_kernel_us": round(us_comb, 3),
         "num_splits": ns,

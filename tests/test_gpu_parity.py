@@ -437,3 +437,32 @@ def test_combine_entry_point_closed_form(out_dtype):
     tol = 1e-2 if out_dtype == torch.bfloat16 else 2e-3
     torch.testing.assert_close(out.cpu().float(), ref.to(out_dtype).float(), atol=tol, rtol=tol)
     torch.testing.assert_close(lse.cpu().double(), M + torch.log(L), atol=1e-5, rtol=1e-5)
+
+
+def test_prepared_call_replays_in_a_hip_graph():
+    """A prepared decode call (split kernel + combine, no memsets or host
+    work inside) captured in a HIP graph: every replay, with eager work and
+    synchronisations in between, equals the eager result."""
+    from dsv4_amd.api import prepare_sparse_attn_sharedkv
+    inp = cases.make_inputs(cases.CONFIGS["C2"], device="cpu")
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    call = prepare_sparse_attn_sharedkv(d.q, **kw)
+    call.launch()
+    torch.cuda.synchronize()
+    ref_out, ref_lse = call.out.clone(), call.lse.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        call.out.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            call.launch(side)
+    torch.cuda.synchronize()
+    for i in range(4):
+        call.out.fill_(float(i + 1))            # eager work between replays
+        call.lse.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(call.out, ref_out) and torch.equal(call.lse, ref_lse), f"replay {i}"
