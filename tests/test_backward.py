@@ -122,6 +122,8 @@ def _gpu_case(name):
         "cfa": dict(B=2, H=16, q_lens=[2, 1], kv_lens=[500, 333], K=0, scenario=2, ratio=8),
         "fp16_d512": dict(B=2, H=16, q_lens=[1, 2], kv_lens=[900, 400], K=64, D=512, dtype=torch.float16),
         "decode_h64": dict(B=8, H=64, q_lens=[1] * 8, kv_lens=[4000, 900, 129, 2500, 60, 3000, 1000, 2048], K=128),
+        # kv shorter than the query: early tokens attend to no row (sink only)
+        "short_kv": dict(B=4, H=32, q_lens=[1, 3, 2, 5], kv_lens=[1, 3, 60, 3], K=32),
     }[name]
     return _small(**spec)
 
@@ -132,7 +134,7 @@ def _rel_err(got, ref):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["C1", "scfa_prefill", "swa", "cfa", "fp16_d512", "decode_h64"])
+@pytest.mark.parametrize("name", ["C1", "scfa_prefill", "swa", "cfa", "fp16_d512", "decode_h64", "short_kv"])
 def test_gpu_backward_matches_oracle(name):
     from dsv4_amd.api import sparse_attn_sharedkv, sparse_attn_sharedkv_backward
     inp = _gpu_case(name)
