@@ -20,9 +20,8 @@
 // atomically. Thread (h, part) sums Delta = dO . O over D / 16 channels of
 // head h (16 lanes, DPP sums). Rows
 // stream through LDS in chunks of 16 (the next chunk's loads in flight in
-// registers): S^T and dP^T are 16x16x32 MFMAs (each head group's four waves
-// take a quarter of the k-steps and add the partial tiles through LDS), P
-// and dS go to an LDS table, then dq (dS . K, accumulated across chunks in
+// registers): S^T and dP^T are 16x16x32 MFMAs (the first wave of each head
+// group computes the group's 16 x 16 tile), P and dS go to an LDS table, then dq (dS . K, accumulated across chunks in
 // registers) and the chunk's dkv rows (dS^T . Q + P^T . dO, summed over the
 // heads, added to the fp32 gradient cache rows with atomics) are 16x16x16
 // MFMAs per 16-channel tile.
@@ -35,6 +34,9 @@ namespace sas {
 namespace {
 
 constexpr int kBwdRows = 16;   // rows per chunk (= lanes per head)
+#ifndef SAS_BWD_NG
+#define SAS_BWD_NG 2   // 16-head groups per workgroup when H is a multiple of 32 (1 or 2)
+#endif
 
 struct BwdParams {
   FwdParams f;
@@ -94,7 +96,6 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_q[NHD * QS];
   __shared__ __attribute__((aligned(16))) uint8_t lds_do[NHD * OS];
   __shared__ float lds_pd[kBwdRows][NHD][2];   // (P, scale dS) per row and head
-  __shared__ f32x4 lds_red[4 * NG][2][64];      // per wave: partial S^T and dP^T tiles
   __shared__ float lds_hd[NHD][2];              // per head: Delta, lse (log2 units)
 
   const FwdParams& p = bp.f;
@@ -195,32 +196,21 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
     }
     __syncthreads();
     if (c0 + kBwdRows < k.nvalid) load_rows(c0 + kBwdRows);
-    // S^T[key][head] = K . Q^T and dP^T = V . dO^T by 16x16x32 MFMA: the
-    // four waves of head group hgw take k-steps wl, wl + 4, ... (A = 8
-    // channels of key c16 from the row tile, B = the same channels of head
-    // c16 from the q / dO tile) and add their partial tiles through LDS;
-    // lane (g4, c16) then holds keys 4 g4 .. + 3 of head c16.
-    {
+    // S^T[key][head] = K . Q^T and dP^T = V . dO^T by 16x16x32 MFMA, the
+    // whole tile in the first wave of head group hgw (A = 8 channels of key
+    // c16 from the row tile, B = the same channels of head c16 from the q /
+    // dO tile); lane (g4, c16) holds keys 4 g4 .. + 3 of head c16 and writes
+    // their P and scale dS to the table.
+    if (wl == 0) {
       f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f}, dacc = sacc;
       const uint8_t* kb = lds_k + c16 * KS + g4 * 16;
       const uint8_t* qb = lds_q + (hgw * 16 + c16) * QS + g4 * 16;
       const uint8_t* ob = lds_do + (hgw * 16 + c16) * OS + g4 * 16;
 #pragma unroll
-      for (int ks = wl; ks < D / 32; ks += 4) {
+      for (int ks = 0; ks < D / 32; ++ks) {
         const uint4 kf = *reinterpret_cast<const uint4*>(kb + ks * 64);
         sacc = mfma32k<QT>(kf, *reinterpret_cast<const uint4*>(qb + ks * 64), sacc);
         if (ks < kDV / 32) dacc = mfma32k<QT>(kf, *reinterpret_cast<const uint4*>(ob + ks * 64), dacc);
-      }
-      lds_red[wave][0][lane] = sacc;
-      lds_red[wave][1][lane] = dacc;
-    }
-    __syncthreads();
-    if (wl == 0) {
-      f32x4 sv = lds_red[hgw * 4][0][lane], dv = lds_red[hgw * 4][1][lane];
-#pragma unroll
-      for (int w = 1; w < 4; ++w) {
-        sv += lds_red[hgw * 4 + w][0][lane];
-        dv += lds_red[hgw * 4 + w][1][lane];
       }
       const int hh = hgw * 16 + c16;
       const float dl = lds_hd[hh][0], l2 = lds_hd[hh][1];
@@ -229,8 +219,8 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
         const int key = 4 * g4 + i;
         float pr = 0.f, dsr = 0.f;
         if (key < nr) {
-          pr = __builtin_amdgcn_exp2f(sv[i] * p.scale_log2 - l2);
-          dsr = pr * (dv[i] - dl) * scale;
+          pr = __builtin_amdgcn_exp2f(sacc[i] * p.scale_log2 - l2);
+          dsr = pr * (dacc[i] - dl) * scale;
         }
         lds_pd[key][hh][0] = pr;
         lds_pd[key][hh][1] = dsr;
@@ -377,7 +367,7 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   // KV splits: the caller's count, else enough (token, head group, split)
   // workgroups for two per CU, each split at least 64 slots
   // two 16-head groups per workgroup when H allows (half the dkv atomics)
-  const int ng = a->H % 32 == 0 ? 2 : 1;
+  const int ng = a->H % 32 == 0 ? SAS_BWD_NG : 1;
   fp.nhg = (int)a->H / (16 * ng);
   int ns = a->num_splits;
   if (ns <= 0) {
