@@ -1087,7 +1087,10 @@ sas_dec_kernel(const FwdParams p) {
 // split-KV combine (separate launch; used with SAS_FWD_NO_COMBINE)
 // ---------------------------------------------------------------------------
 
-constexpr int kCombineThreads = 256;
+#ifndef SAS_COMBINE_THREADS
+#define SAS_COMBINE_THREADS 256
+#endif
+constexpr int kCombineThreads = SAS_COMBINE_THREADS;
 constexpr int kMaxCombineSplits = 64;
 
 // One workgroup per (token, 4 heads), thread = (head, 8 channels): 16-byte
