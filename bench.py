@@ -87,6 +87,65 @@ def time_launches(launch, n_calls, steps, warmup):
     return e0.elapsed_time(e1), wall
 
 
+def time_cold(launch, steps, flush):
+    """Per-call event time with the caches flushed before every call: a
+    read of a 1 GB buffer (leaving the 256 MB MALL and the L2s holding other
+    lines) runs before each call's start event, outside the timed span.
+    Returns the median call in ms."""
+    st = torch.cuda.current_stream()
+    evs = []
+    for _ in range(steps):
+        flush()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        launch(st)
+        e1.record(st)
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in evs)
+    return ts[len(ts) // 2]
+
+
+def measured_peaks():
+    """HBM: a 2 GiB device copy (read + write bytes / time); bf16 MFMA: an
+    8192^3 bf16 GEMM through torch (hipBLASLt)."""
+    n = 1 << 29                                     # 2 GiB of fp32
+    src = torch.empty(n, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    ms, _ = time_launches(lambda i, st: dst.copy_(src), 1, 20, 3)
+    copy_gbs = 2 * n * 4 / (ms / 20 * 1e-3) / 1e9
+    del src, dst
+    m = 8192
+    a = torch.randn(m, m, device="cuda").to(torch.bfloat16)
+    b = torch.randn(m, m, device="cuda").to(torch.bfloat16)
+    c = torch.empty(m, m, device="cuda", dtype=torch.bfloat16)
+    ms, _ = time_launches(lambda i, st: torch.matmul(a, b, out=c), 1, 20, 3)
+    gemm_tf = 2 * m ** 3 / (ms / 20 * 1e-3) / 1e12
+    del a, b, c
+    torch.cuda.synchronize()
+    return dict(hbm_spec_gbs=HBM_PEAK_GBS, hbm_copy_measured_gbs=round(copy_gbs, 1),
+                bf16_spec_tflops=BF16_PEAK_TFLOPS, bf16_gemm_measured_tflops=round(gemm_tf, 1),
+                how="copy: torch copy_ of 2 GiB (read + write bytes); gemm: torch.matmul 8192^3 bf16")
+
+
+def usable_cores():
+    """Cores this process may run on: the affinity set, capped by the
+    cgroup CPU quota when one is set (a job's CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    note = f"{n} in the affinity set"
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            q = max(1, int(int(quota) / int(period)))
+            if q < n:
+                note += f", cgroup quota {q}"
+                n = q
+    except (OSError, ValueError):
+        pass
+    return n, note
+
+
 def cpu_oracle_time(inp, tokens=None, min_seconds=0.0, max_reps=1):
     """Median seconds of one oracle pass; repeats until min_seconds of CPU
     work (or max_reps passes) have run."""
@@ -248,6 +307,36 @@ def bench_cache_write(traffic=None):
                 _log=f"cache write: {us:.2f} us/call, {gbs:.0f} GB/s ({byts} B)")
 
 
+def bench_decode_configs(names, steps, flush):
+    """C1 / C4 / C5 (and C2 for comparison): one whole call per timed span,
+    caches flushed before each. Algorithmic bytes = valid (token, key) rows
+    x row bytes (1152 for bf16 rows at D = 576, 656 for fp8 rows)."""
+    from dsv4_amd import cases
+    res = {}
+    for name in names:
+        cfg = cases.CONFIGS[name]
+        inp = cases.make_inputs(cfg, device="cuda")
+        rows = cases.gathered_rows(inp)
+        rb = 656 if cfg.fp8 else cfg.D * 2
+        call = _prepare(inp)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            call.launch()
+        ms = time_cold(lambda st: call.launch(st), steps, flush)
+        us = ms * 1e3
+        byts = rows * rb
+        gbs = byts / (us * 1e-6) / 1e9
+        res[name] = dict(workload=cfg.notes, tokens=inp.T, gathered_rows=rows, row_bytes=rb,
+                         gathered_bytes=byts, us_per_call=round(us, 3), gbs=round(gbs, 1),
+                         hbm_frac=round(gbs / HBM_PEAK_GBS, 4), splits=call.num_splits,
+                         timing="median of per-call events, caches flushed before each call")
+        log(f"{name}: {us:.2f} us/call (cold), {gbs:.0f} GB/s on {byts} gathered bytes, "
+            f"splits {call.num_splits}")
+        del call, inp
+        torch.cuda.synchronize()
+    return res
+
+
 BWD_FLOP_PER_PAIR_HEAD = 2 * (3 * 576 + 2 * 512)   # q.k, dO.v, dq, dk (D = 576), dv (512)
 
 
@@ -258,7 +347,7 @@ def bench_backward(dec_inp, pre_inp):
     FLOP per (token, key, head): 2 x (3 x 576 + 2 x 512) = 5504."""
     from dsv4_amd import cases
     from dsv4_amd.api import prepare_sparse_attn_sharedkv_backward, sparse_attn_sharedkv
-    res = {"kernel": "sas_bwd_kernel (VALU fp32, first version)",
+    res = {"kernel": "sas_bwd_kernel (MFMA scores, dq and dkv; fp32 atomics for dkv)",
            "flop_per_pair_head": BWD_FLOP_PER_PAIR_HEAD}
     for key, inp, steps in (("decode", dec_inp, 50), ("prefill", pre_inp, 3)):
         if inp is None:
@@ -291,6 +380,8 @@ def main():
     ap.add_argument("--no-traffic", action="store_true")
     ap.add_argument("--no-cache-write", action="store_true")
     ap.add_argument("--no-backward", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C4 / C5 decode lines")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured copy / GEMM peaks")
     ap.add_argument("--pmc-pass", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -398,6 +489,22 @@ def main():
                        mfma_frac=round(tfl / BF16_PEAK_TFLOPS, 4), splits=pcall.num_splits)
         log(f"C3 prefill: {pus:.1f} us/call, {tfl:.1f} TFLOP/s ({flops:.4e} useful FLOP)")
 
+    # ---------------- the other decode configs (cold caches) ----------------
+    flush_buf = torch.empty(1 << 28, device="cuda").normal_()     # 1 GiB
+
+    def flush():
+        flush_buf.sum()
+
+    configs = None
+    if not args.no_configs:
+        configs = bench_decode_configs(["C1", "C2", "C4", "C5"], 50, flush)
+
+    peaks = None
+    if not args.no_peaks:
+        peaks = measured_peaks()
+        log(f"peaks: copy {peaks['hbm_copy_measured_gbs']} GB/s, "
+            f"bf16 GEMM {peaks['bf16_gemm_measured_tflops']} TFLOP/s")
+
     # ---------------- backward (C2 decode, C3 prefill) ----------------------
     backward = None
     if not args.no_backward:
@@ -416,22 +523,21 @@ def main():
     # ---------------- CPU baseline (oracle on host cores) --------------------
     cpu = None
     if not args.no_cpu:
-        n = min(len(os.sched_getaffinity(0)), 16)
+        n, core_note = usable_cores()
         torch.set_num_threads(n)
-        log(f"CPU baseline on {n} threads")
+        log(f"CPU baseline on {n} threads ({core_note})")
         host = inp.to("cpu")
         cpu_s, reps, spent = cpu_oracle_time(host, min_seconds=10.0, max_reps=1000)
         cpu = dict(value=round(kv_bytes / cpu_s / 1e9, 3), unit="GB/s", cores=n, kind="port",
-                   us_per_call=round(cpu_s * 1e6, 1),
+                   cores_note=core_note, us_per_call=round(cpu_s * 1e6, 1),
                    sample=f"full C2 decode call (32 tokens x 64 heads), median of {reps} calls "
                           f"({spent:.1f} s), torch fp32 oracle")
         if prefill is not None:
             ph = pinp.to("cpu")
-            toks = list(range(0, pinp.T, 8))
-            ps1, _, _ = cpu_oracle_time(ph, tokens=toks)
-            ps = ps1 * pinp.T / len(toks)
+            ps, _, _ = cpu_oracle_time(ph)
             cpu["prefill_tflops"] = round(prefill["useful_flop"] / ps / 1e12, 4)
-            cpu["prefill_sample"] = f"{len(toks)} of {pinp.T} C3 tokens (every 8th), scaled"
+            cpu["prefill_s"] = round(ps, 2)
+            cpu["prefill_sample"] = f"one full C3 pass ({pinp.T} tokens)"
 
     tr = None
     if traffic:
@@ -465,6 +571,8 @@ def main():
                      "kernel": f"{SPLIT_KERNEL} (C2 split-KV forward, {ns} splits)",
                      "traffic_detail": traffic if traffic else traffic_note},
         "prefill": prefill,
+        "decode_configs": configs,
+        "peaks": peaks,
         "cache_write": cwrite,
         "backward": backward,
         "cpu_baseline": cpu,

@@ -31,9 +31,20 @@ class PreparedCacheWrite:
         self.args = args
         self._keep = keep
         self.device = device
+        # the int32 / contiguous conversions were enqueued on this stream
+        self._prep_stream = torch.cuda.current_stream(device)
 
     def launch(self, stream: Optional[torch.cuda.Stream] = None) -> None:
         st = stream if stream is not None else torch.cuda.current_stream(self.device)
+        if st != self._prep_stream:
+            # order the launch after the conversions, and keep every bound
+            # tensor's memory from being reused by the caching allocator on
+            # its own stream while the kernel on `st` may still touch it
+            ev = torch.cuda.Event()
+            ev.record(self._prep_stream)
+            st.wait_event(ev)
+            for t in self._keep:
+                t.record_stream(st)
         _lib.check(_lib.lib().sas_cache_write_v1(C.byref(self.args), C.c_void_p(st.cuda_stream)),
                    "write_kv_cache")
 

@@ -326,7 +326,6 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   if (a->win_left < 0 || a->win_left > 8191) return set_error(SAS_EINVAL, "bwd: win_left out of range");
   if (a->scenario >= SAS_CFA && (a->cmp_ratio < 1 || a->K < 0)) return set_error(SAS_EINVAL, "bwd: bad cmp_ratio/K");
   const long long nslots = a->win_left + 1 + (a->scenario >= SAS_CFA ? a->K : 0);
-  if (nslots > kMaxSlots) return set_error(SAS_EINVAL, "bwd: at most %d key slots per token (got %lld)", kMaxSlots, nslots);
   if (a->T == 0) return SAS_OK;
   if (!a->q || !a->ori_kv || !a->ori_block_table || !a->q_prefix || !a->act_q || !a->act_kv || !a->sinks ||
       !a->out || !a->lse || !ba->dout || !ba->dq || !ba->d_ori_kv || !ba->d_sinks)
@@ -377,9 +376,16 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
     ns = (int)std::min<long long>(want, (nslots + 63) / 64);
   }
   ns = std::max(1, std::min(ns, 64));
-  const int sps = (int)((nslots + ns - 1) / ns);
+  long long sps = (nslots + ns - 1) / ns;
+  if (sps > kMaxSlots) {
+    // a workgroup resolves at most kMaxSlots slots: more splits (dq is then
+    // accumulated atomically across them)
+    ns = (int)((nslots + kMaxSlots - 1) / kMaxSlots);
+    if (ns > 64) return set_error(SAS_EINVAL, "bwd: too many key slots per token (%lld)", nslots);
+    sps = (nslots + ns - 1) / ns;
+  }
   fp.nsplit = (int)((nslots + sps - 1) / sps);
-  fp.slots_per_split = sps;
+  fp.slots_per_split = (int)sps;
   bp.out = (const uint8_t*)a->out;
   bp.dout = (const uint8_t*)ba->dout;
   bp.dq = ba->dq;

@@ -620,6 +620,64 @@ struct Fwd {
     }
   }
 
+  // -- exact-window schedule (4 waves, at most kLdsRows rows, one split) -----
+  // Every key-group's rows fit its NST slots (KW x NST x TR = kLdsRows), so
+  // the whole row set is gathered at once and stays resident. QK^T runs
+  // twice over it: first for each head's maximum over all rows and the sink
+  // (key-groups exchange theirs through LDS), then for P, which is thus
+  // rounded against the final maximum of the tile, as golden rounds its
+  // single window tile (golden.py:178-195) and as the reference kernel runs
+  // a 128-row window as one chunk (kernel.py:83, 97-100, 1743). Used for the
+  // window-only scenario, whose key set is that one tile.
+  __device__ __forceinline__ void run_exact(int wave, float sink_log2) {
+    static_assert(NW == 4 && C::KW * C::NST * C::TR == kLdsRows, "exact schedule: the ring holds every row");
+    if constexpr (!KVF) {
+#pragma unroll
+      for (int j = 0; j < C::NST; ++j)
+        if (j < nsteps) issue(j, j);
+      wait_vm<0>();
+    } else {
+#pragma unroll
+      for (int j = 0; j < C::NST; ++j)
+        if (j < nsteps) { fload(j); fstore(j); }
+    }
+    lds_barrier();
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < C::NST; ++j) {
+      if (j >= nsteps) break;   // uniform over the key-group's waves
+      f32x4 sacc[C::MT], sodd[C::MT];
+      qk(slot(j), sacc, sodd, [](int) {});
+      const int nk = min(C::TR, nrows - j * C::TR);
+#pragma unroll
+      for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (mt * 16 + g * 4 + i < nk) mloc = fmaxf(mloc, (sacc[mt][i] + sodd[mt][i]) * p.scale_log2);
+    }
+    mloc = rows_max(mloc);
+    if constexpr (C::KW > 1) {
+      if (g == 0) lds_ml[wave][0][c16] = mloc;
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < C::KW; ++j) mloc = fmaxf(mloc, lds_ml[j * C::WK + jw][0][c16]);
+      __syncthreads();   // read before the epilogue reuses lds_ml
+    }
+    // every key-group rounds against M = max(sink, all rows); the sink's
+    // (1 at its own maximum) term is counted once, by key-group 0
+    m_run = fmaxf(mloc, sink_log2);
+    l_run = kw == 0 ? __builtin_amdgcn_exp2f(sink_log2 - m_run) : 0.f;
+#pragma unroll
+    for (int j = 0; j < C::NST; ++j) {
+      if (j >= nsteps) break;
+      f32x4 sacc[C::MT], sodd[C::MT];
+      uint32_t pk[2 * C::MT];
+      qk(slot(j), sacc, sodd, [](int) {});
+      smax(sacc, sodd, j, pk);
+      pv(slot(j), pk, [](int) {});
+    }
+  }
+
   __device__ __forceinline__ void run() {
     if constexpr (kPipe) {
       run_pipe();
@@ -812,7 +870,8 @@ __device__ __forceinline__ void epilogue(const FwdParams& p, const Tok& k, int t
 // forward kernel, head-waves sharing LDS tiles (HW = 2, 4)
 // ---------------------------------------------------------------------------
 
-template <int HW, int NW, int D, typename QT, int KVF>
+// EXW: the exact-window schedule (Fwd::run_exact) instead of the streaming loop
+template <int HW, int NW, int D, typename QT, int KVF, bool EXW>
 __global__ void __launch_bounds__(NW * 64)
 sas_fwd_kernel(const FwdParams p) {
   using C = Cfg<HW, NW, D, QT, KVF>;
@@ -854,7 +913,7 @@ sas_fwd_kernel(const FwdParams p) {
   // retire every load the compiler tracks (Q, tables, indices, sink) before
   // the DMA ring starts, so none of its own vmcnt waits lands inside the loop
   const bool seed_sink = p.nsplit == 1 && f.kw == 0;
-  const float sink = seed_sink ? p.sinks[hq] : 0.f;
+  const float sink = (seed_sink || EXW) ? p.sinks[hq] : 0.f;
   __builtin_amdgcn_s_waitcnt(0);
   if constexpr (C::QL) {
     __syncthreads();   // every wave's query DMA has landed
@@ -865,7 +924,8 @@ sas_fwd_kernel(const FwdParams p) {
 #pragma unroll
   for (int i = 0; i < C::NTL; ++i) f.acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  f.run();
+  if constexpr (EXW) f.run_exact(wave, sink * kLog2e);
+  else f.run();
   epilogue<HW, NW, C::CS, QT>(p, k, tid, wave, lane, f.m_run, f.l_run, f.acc);
 }
 
@@ -1119,6 +1179,7 @@ int part_bytes(int q_dtype) { return q_dtype == SAS_DT_FP16 ? 4 : 2; }
 
 struct Plan {
   int hw, nw, nhg, nslots, nsplit, sps;
+  bool exact;   // exact-window schedule (Fwd::run_exact)
   size_t ws;
 };
 
@@ -1136,6 +1197,11 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   const long long T = std::max<long long>(a->T, 1);
   int hw = a->head_waves;
   int ns = a->num_splits;
+  // Window-only calls whose window fits the ring run the exact-window
+  // schedule: one split, 4 waves, P rounded against the window's final
+  // maximum (golden's one window tile). An explicit split count above 1 or
+  // 8 waves selects the streaming schedule instead.
+  pl->exact = a->scenario == SAS_SWA && pl->nslots <= kLdsRows && ns <= 1 && (a->waves == 0 || a->waves == 4);
   if (hw <= 0) {
     // Heads sharing one gathered tile inside a workgroup (16 per wave). With
     // many tokens every workgroup holds 64 heads: each row crosses L2 -> CU
@@ -1159,10 +1225,11 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   if (nw == 8 && fp8) nw = 4;
   if (nw <= 0) nw = (hw >= 2 && !fp8) ? 8 : 4;
   if (nw != 4 && nw != 8) return sas::set_error(SAS_EINVAL, "waves must be 4 or 8");
-  if (hw == 1) nw = 4;
+  if (hw == 1 || pl->exact) nw = 4;
   pl->nw = nw;
   pl->hw = hw;
   pl->nhg = (int)a->H / (16 * hw);
+  if (pl->exact) ns = 1;
   if (ns <= 0) {
     // one workgroup per CU: split the slots until the grid covers the chip,
     // keeping every split long enough for one step of each key-group
@@ -1186,9 +1253,9 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   return SAS_OK;
 }
 
-template <int HW, int NW, int D, typename QT, int KVF>
+template <int HW, int NW, int D, typename QT, int KVF, bool EXW = false>
 int launch_fwd(const FwdParams& fp, int nblocks, hipStream_t st) {
-  hipLaunchKernelGGL((sas_fwd_kernel<HW, NW, D, QT, KVF>), dim3(nblocks), dim3(NW * 64), 0, st, fp);
+  hipLaunchKernelGGL((sas_fwd_kernel<HW, NW, D, QT, KVF, EXW>), dim3(nblocks), dim3(NW * 64), 0, st, fp);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return sas::set_error(SAS_ELAUNCH, "sas_fwd launch: %s", hipGetErrorString(e));
   return SAS_OK;
@@ -1203,7 +1270,13 @@ int launch_dec(const FwdParams& fp, int nblocks, hipStream_t st) {
 }
 
 template <int D, typename QT, int KVF>
-int dispatch_hw(int hw, int nw, const FwdParams& fp, int nb, hipStream_t st) {
+int dispatch_hw(int hw, int nw, bool exact, const FwdParams& fp, int nb, hipStream_t st) {
+  if (exact) {
+    if (hw == 1) return launch_fwd<1, 4, D, QT, KVF, true>(fp, nb, st);
+    if (hw == 2) return launch_fwd<2, 4, D, QT, KVF, true>(fp, nb, st);
+    if (hw == 4) return launch_fwd<4, 4, D, QT, KVF, true>(fp, nb, st);
+    return sas::set_error(SAS_EINVAL, "unsupported head grouping");
+  }
   if (hw == 1) return launch_dec<D, QT, KVF>(fp, nb, st);
   if (hw == 2 && nw == 4) return launch_fwd<2, 4, D, QT, KVF>(fp, nb, st);
   if (hw == 2 && nw == 8) return launch_fwd<2, 8, D, QT, KVF>(fp, nb, st);
@@ -1320,13 +1393,13 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   fp.out_nt = pl.nsplit == 1 && (size_t)a->T * a->H * kDV * 2 >= (size_t(16) << 20);
   hipStream_t st = (hipStream_t)stream;
 
-  if (fp8) rc = dispatch_hw<576, __bf16, 1>(pl.hw, pl.nw, fp, nblocks, st);
+  if (fp8) rc = dispatch_hw<576, __bf16, 1>(pl.hw, pl.nw, pl.exact, fp, nblocks, st);
   else if (a->q_dtype == SAS_DT_BF16)
-    rc = a->D == 576 ? dispatch_hw<576, __bf16, 0>(pl.hw, pl.nw, fp, nblocks, st)
-                     : dispatch_hw<512, __bf16, 0>(pl.hw, pl.nw, fp, nblocks, st);
+    rc = a->D == 576 ? dispatch_hw<576, __bf16, 0>(pl.hw, pl.nw, pl.exact, fp, nblocks, st)
+                     : dispatch_hw<512, __bf16, 0>(pl.hw, pl.nw, pl.exact, fp, nblocks, st);
   else
-    rc = a->D == 576 ? dispatch_hw<576, _Float16, 0>(pl.hw, pl.nw, fp, nblocks, st)
-                     : dispatch_hw<512, _Float16, 0>(pl.hw, pl.nw, fp, nblocks, st);
+    rc = a->D == 576 ? dispatch_hw<576, _Float16, 0>(pl.hw, pl.nw, pl.exact, fp, nblocks, st)
+                     : dispatch_hw<512, _Float16, 0>(pl.hw, pl.nw, pl.exact, fp, nblocks, st);
   if (rc || pl.nsplit == 1 || (a->flags & SAS_FWD_NO_COMBINE)) return rc;
   return launch_combine(fp, a->q_dtype, st);
 }

@@ -99,7 +99,7 @@ typedef struct SasFwdArgs {
   const float* sinks;            /* [H] */
   void* out;                     /* [T, H, DV] q_dtype */
   float* lse;                    /* [T, H] */
-  void* workspace;               /* split-KV partials, see sas_fwd_workspace_size */
+  void* workspace;               /* split-KV partials; size from sas_fwd_plan */
   size_t workspace_bytes;
   int64_t T, B, H, D, DV;
   int64_t ori_block_size, ori_bt_stride, ori_num_blocks;
@@ -181,8 +181,8 @@ int sas_combine_v1(const SasCombineArgs* a, void* stream);
  *   d_sinks[h] += -exp(sink_h - lse) Delta         (accumulated)
  * All four outputs must be zeroed by the caller first; cache rows (and dq
  * with several KV splits) receive atomic fp32 adds, so their summation order
- * varies.
- * At most 1280 key slots per token (win_left + 1 + K).
+ * varies. Tokens with more than 1280 key slots (win_left + 1 + K) are split
+ * across several workgroups.
  */
 typedef struct SasBwdArgs {
   SasFwdArgs fwd;

@@ -34,9 +34,11 @@ def _rows(bt_row, positions, bs):
 
 def backward_paged(q, dout, *, ori_kv, ori_block_table, cu_seqlens_q, seqused_kv, sinks, softmax_scale,
                    cmp_kv=None, cmp_block_table=None, cmp_sparse_indices=None, cmp_ratio=None,
-                   ori_win_left=127, dv=512, drop_sink: bool = False):
+                   ori_win_left=127, dv=512, drop_sink: bool = False, tokens=None):
     """Returns dict(out, lse, dq [T,H,D], d_ori=(rows, grads), d_cmp=(rows, grads) or None,
-    d_sinks [H]) in fp64. ``drop_sink`` plants a mistake for the oracle's own tests."""
+    d_sinks [H]) in fp64. ``drop_sink`` plants a mistake for the oracle's own tests.
+    ``tokens`` restricts the loss to those packed token ids (the others have
+    zero out / lse / dq and contribute nothing, as if their dout were zero)."""
     q = q.detach().cpu().double()
     dout = dout.detach().cpu().double()
     T, H, D = q.shape
@@ -49,10 +51,13 @@ def backward_paged(q, dout, *, ori_kv, ori_block_table, cu_seqlens_q, seqused_kv
     cbs = cmp_kv.shape[1] if cmp_kv is not None else 1
     # per token: (ori rows, cmp rows) in golden's order
     plan = {}
+    want = None if tokens is None else set(int(x) for x in tokens)
     for b in range(len(cu) - 1):
         aq, akv = cu[b + 1] - cu[b], kvl[b]
         for s in range(aq):
             t = cu[b] + s
+            if want is not None and t not in want:
+                continue
             sg = akv - aq + s
             lo = max(sg - ori_win_left, 0)
             orows = _rows(obt[b], list(range(lo, sg + 1)), obs)

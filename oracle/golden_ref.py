@@ -53,13 +53,17 @@ def _cmp_rows(idx_row: Sequence[int], threshold: int, cmp_len: int) -> list:
 
 
 def _attend(q: torch.Tensor, tiles, sinks: torch.Tensor, scale: float, dtype, dv: int,
-            exact: bool = False):
+            exact: bool = False, scores_fp64: bool = False):
     """Chunked sink-seeded online softmax for one token (golden.py:156-200).
 
     ``q`` [G, D] fp32, ``tiles`` list of fp32 [n, D] (already in walk order).
     Returns (out [G, dv] in ``dtype``, lse [G] fp32). With ``exact`` the same
     walk runs in fp64 with no rounding of ``p`` or of the output (a reference
-    point for how far golden's own bf16/fp16 roundings move it).
+    point for how far golden's own bf16/fp16 roundings move it). With
+    ``scores_fp64`` the fp32 walk is unchanged except that ``q k^T`` is
+    evaluated in fp64 and rounded once to fp32: an equally valid fp32 score
+    (another summation order), used to measure how much golden's output
+    depends on the order in which its scores are summed.
     """
     G = q.shape[0]
     wt = torch.float64 if exact else torch.float32
@@ -71,7 +75,7 @@ def _attend(q: torch.Tensor, tiles, sinks: torch.Tensor, scale: float, dtype, dv
         if k.shape[0] == 0:
             continue
         k = k.to(wt)
-        sc = (q @ k.T) * scale
+        sc = ((q.double() @ k.double().T).to(wt) if scores_fp64 else q @ k.T) * scale
         m_new = torch.maximum(m, sc.amax(dim=1))
         alpha = torch.exp(m - m_new)
         p = torch.exp(sc - m_new.unsqueeze(1))
@@ -105,7 +109,12 @@ def golden_bnsd(q_bnsd, ori_k_bnsd, sinks, *, act_q_lens, act_kv_lens, softmax_s
         aq, akv = int(act_q_lens[b]), int(act_kv_lens[b])
         for s in range(aq):
             sg = akv - aq + s
-            win = ori_k_bnsd[b, 0, max(sg - ori_win_left, 0):sg + 1].float()
+            # window [max(sg - win_left, 0), sg]: empty for sg < 0, as the
+            # reference kernel's mask idx <= s_global gives (kernel.py:273-276).
+            # golden.py:128-131 slices ori_k[left:sg + 1], which for
+            # sg < -1 ends at a negative index and takes rows from the end of
+            # the cache (a slicing artefact, not the operator's semantics).
+            win = ori_k_bnsd[b, 0, max(sg - ori_win_left, 0):max(sg + 1, 0)].float()
             parts = _tiles(win, s2_tile) if win.shape[0] else []
             if cmp_k_bnsd is not None:
                 thr = (sg + 1) // cmp_ratio
@@ -136,7 +145,7 @@ def _paged_rows(kv, bt_row, positions, dequant):
 def golden_paged(q, *, ori_kv, ori_block_table, cu_seqlens_q, seqused_kv, sinks,
                  softmax_scale, cmp_kv=None, cmp_block_table=None, cmp_sparse_indices=None,
                  cmp_ratio=None, ori_win_left=127, dv=512, dequant=None, tokens=None,
-                 s2_tile: int = GOLDEN_S2_TILE, exact: bool = False):
+                 s2_tile: int = GOLDEN_S2_TILE, exact: bool = False, scores_fp64: bool = False):
     """TND / paged-cache oracle: same math as :func:`golden_bnsd`, rows read
     through block tables (only the rows a token touches are materialised).
 
@@ -175,7 +184,7 @@ def golden_paged(q, *, ori_kv, ori_block_table, cu_seqlens_q, seqused_kv, sinks,
                 else:
                     sel = list(range(max(thr, 0)))
                 parts += _tiles(_paged_rows(cmp_kv, cmp_bt[b], sel, dequant), s2_tile)
-            o, l_ = _attend(q[t].float(), parts, sinks, softmax_scale, dtype, dv, exact)
+            o, l_ = _attend(q[t].float(), parts, sinks, softmax_scale, dtype, dv, exact, scores_fp64)
             out[t] = o
             lse[t] = l_
     return out, lse

@@ -202,3 +202,26 @@ def test_gpu_cache_write_strided_rows_and_empty_call():
     write_kv_cache(dw[:0, :576], d, table.cuda(), sid.cuda()[:0], pos.cuda()[:0])
     torch.cuda.synchronize()
     assert torch.equal(d.cpu(), ref)
+
+
+@pytest.mark.gpu
+def test_gpu_cache_write_int64_indices_on_a_side_stream():
+    """int64 seq_ids / positions (converted on the current stream) with the
+    kernel launched on another stream: the launch waits for the conversions,
+    and the converted temporaries stay allocated until it has run (the
+    current stream's next allocations cannot reuse them meanwhile)."""
+    from dsv4_amd.cache import write_kv_cache
+    kv, cache, table, sid, pos = _case(torch.bfloat16, True, N=600, seed=11)
+    ref = R.write_kv_cache_ref(kv, cache, table, sid, pos)
+    d = cache.cuda()
+    dkv, dt = kv.cuda(), table.cuda().to(torch.int64)
+    dsid, dpos = sid.cuda().to(torch.int64), pos.cuda().to(torch.int64)
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    torch.cuda._sleep(2_000_000)            # the current stream is busy when the conversions queue
+    write_kv_cache(dkv, d, dt, dsid, dpos, stream=side)
+    junk = [torch.full((600,), -7, dtype=torch.int32, device="cuda") for _ in range(8)]
+    side.synchronize()
+    torch.cuda.synchronize()
+    del junk
+    assert torch.equal(d.cpu(), ref), f"{int((d.cpu() != ref).sum())} bytes differ"

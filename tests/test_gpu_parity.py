@@ -171,17 +171,12 @@ REF_CASES = [("scfa_decode", None), ("swa_decode", None), ("cfa_decode", None),
 
 
 # The reference rule (>= 99.5 % of elements within bf16 rtol 2^-7) measures
-# agreement with golden's own rounding of p to bf16, which golden does
-# relative to the running max after each 512-row tile (golden.py:156-196).
-# The kernel rounds p relative to the reference max of each KV split and
-# key-group: a different rounding pattern, no less accurate. For swa_decode
-# in bf16 (one token, 32,768 outputs) that alone moves the agreement just
-# below 99.5 %; the test requires the output to be at least as close to the
-# fp64 exact result as golden's is, and at least RULE_FLOOR % of elements
-# within the rule's tolerance, and then records the miss as an expected
-# failure.
-RULE_KNOWN_MISS = {("swa_decode", torch.bfloat16)}
-RULE_FLOOR = 99.0
+# agreement with golden's own rounding of p to the query dtype, which golden
+# does relative to the running max after each 512-row tile
+# (golden.py:156-196). Window-only calls run the exact-window schedule (p
+# rounded against the window's final max, golden's one tile), so swa_decode
+# reproduces golden's rounding; the compressed scenarios round against each
+# KV split's own reference max and meet the rule with margin.
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
@@ -198,35 +193,37 @@ def test_reference_scenarios(name, s1, dtype):
           f"golden {e_gold:.4g}", flush=True)
     assert e_ours <= 1.10 * e_gold + 1e-6, f"{name}: less accurate than golden"
     torch.testing.assert_close(lse.double(), ex_lse, atol=1e-5, rtol=2e-6)
+    # The BASELINE tolerance on every element: LSE within 1e-3 of golden; the
+    # output within atol = rtol = 2e-2 of golden's formula evaluated in fp64.
+    # On this U(-10,10) data golden's own output moves by more than 2e-2 at
+    # cancellation points when only its fp32 score summation order changes
+    # (tests/test_oracle.py::test_golden_depends_on_score_summation_order_*),
+    # so two correct implementations can differ by that much; golden itself
+    # meets the bound against the fp64 result, and so must the kernel.
+    torch.testing.assert_close(lse, ref_lse, atol=LSE_ATOL, rtol=0.0,
+                               msg=lambda m: f"{name} lse vs golden: {m}")
+    _check_baseline(out, lse, ex_out, ex_lse.float(), f"{name} {dtype} vs fp64")
+    far = (out.float() - ref_out.float()).abs() > OUT_TOL + OUT_TOL * ref_out.float().abs()
+    print(f"[parity] {name}: {int(far.sum())} of {far.numel()} elements beyond 2e-2 of golden", flush=True)
     if dtype == torch.bfloat16:
         rules = [(out, ref_out, 0.0078125, 1e-4, "out"), (lse, ref_lse, 0.015, 0.005, "lse")]
     else:
         rules = [(out, ref_out, 0.005, 2.5e-5, "out"), (lse, ref_lse, 0.01, 0.001, "lse")]
-    missed = []
     for real, expt, rt, at, what in rules:
         pct, worst, n_err = _reference_rule(real, expt, rt, at)
         print(f"[parity] {name} {what}: {pct:.3f}% within, worst {worst:.3f}", flush=True)
-        if pct < 99.5 or worst >= 10.0:
-            missed.append(f"{what} {pct:.3f}% within (worst {worst:.3f})")
-    if missed and (name, dtype) in RULE_KNOWN_MISS:
-        for real, expt, rt, at, what in rules:
-            pct, worst, _ = _reference_rule(real, expt, rt, at)
-            assert pct >= RULE_FLOOR and worst < 10.0, f"{name} {what}: {pct:.3f}% within"
-        pytest.xfail(f"{name}: reference rule vs golden's p rounding: {'; '.join(missed)}")
-    assert not missed, f"{name}: " + "; ".join(missed)
+        _check_reference_rule(real, expt, rt, at, f"{name} {what}")
 
 
-def test_reference_scenario_8k_prefill_sampled():
-    """scfa_prefill at its full 8192 tokens; the oracle checks a spread of
-    512 tokens (first, last, block edges, random)."""
+def test_reference_scenario_8k_prefill():
+    """scfa_prefill at its full 8192 tokens, every token checked against the
+    oracle: the reference's rule and the BASELINE tolerance."""
     inp = cases.ref_case("scfa_prefill", dtype=torch.bfloat16)
     out, lse, _ = _run(inp)
-    g = torch.Generator().manual_seed(0)
-    toks = sorted(set([0, 1, 2, 126, 127, 128, 129, 511, 512, 513, 8190, 8191] +
-                      torch.randint(0, 8192, (500,), generator=g).tolist()))
-    ref_out, ref_lse = _oracle(inp, tokens=toks)
-    _check_reference_rule(out[toks], ref_out[toks], 0.0078125, 1e-4, "scfa_prefill out")
-    _check_reference_rule(lse[toks], ref_lse[toks], 0.015, 0.005, "scfa_prefill lse")
+    ref_out, ref_lse = _oracle(inp)
+    _check_reference_rule(out, ref_out, 0.0078125, 1e-4, "scfa_prefill out")
+    _check_reference_rule(lse, ref_lse, 0.015, 0.005, "scfa_prefill lse")
+    torch.testing.assert_close(lse, ref_lse, atol=LSE_ATOL, rtol=0.0)
 
 
 def test_api_return_type():
@@ -347,6 +344,16 @@ EDGE = {
     # block size 128, an odd top-k width, H = 128 in fp16
     "bs128_k77": dict(B=3, H=64, q_lens=[1, 2, 1], kv_lens=[3000, 777, 129], K=77, bs=128),
     "h128_fp16": dict(B=2, H=128, q_lens=[2, 1], kv_lens=[2500, 1000], K=256, dtype=torch.float16),
+    # window-only calls: the exact-window schedule with 16, 32 and 64 heads
+    # per workgroup, fp8 rows, a 64-row window, a padded BSND-like short
+    # cache; a 201-row window exceeds the ring and streams instead
+    "swa_h16": dict(B=2, H=16, q_lens=[1, 3], kv_lens=[200, 60], K=0, scenario=1),
+    "swa_h48_d512_fp16": dict(B=2, H=48, q_lens=[2, 1], kv_lens=[900, 130], K=0, scenario=1, D=512,
+                              dtype=torch.float16),
+    "swa_h32_win63": dict(B=2, H=32, q_lens=[4, 1], kv_lens=[700, 64], K=0, scenario=1, win=63),
+    "swa_fp8": dict(B=2, H=64, q_lens=[1, 2], kv_lens=[3000, 90], K=0, scenario=1, fp8=True),
+    "swa_prefill_h128": dict(B=1, H=128, q_lens=[300], kv_lens=[300], K=0, scenario=1),
+    "swa_win200": dict(B=2, H=64, q_lens=[2, 1], kv_lens=[1000, 150], K=0, scenario=1, win=200),
 }
 
 
@@ -369,6 +376,24 @@ def test_edge_cases(name):
     out, lse, _ = _run(inp)
     ref_out, ref_lse = _oracle(ref_inp)
     _check_baseline(out, lse, ref_out, ref_lse, name)
+
+
+def test_swa_exact_and_streaming_schedules_agree():
+    """Window-only decode: the exact-window schedule (one split, p rounded
+    against the window's final max) and the streaming schedule (forced by
+    an explicit split count) both meet the tolerance; the exact one is at
+    least as close to golden, whose rounding it reproduces."""
+    inp = _small(B=3, H=64, q_lens=[1, 1, 2], kv_lens=[4000, 128, 777], K=0, scenario=1, seed=3)
+    ref_out, ref_lse = _oracle(inp)
+    ex_out, ex_lse, ns1 = _run(inp)
+    st_out, st_lse, ns2 = _run(inp, num_splits=2)
+    assert ns1 == 1 and ns2 == 2
+    _check_baseline(ex_out, ex_lse, ref_out, ref_lse, "swa exact")
+    _check_baseline(st_out, st_lse, ref_out, ref_lse, "swa streaming")
+    e_ex = float((ex_out.float() - ref_out.float()).abs().mean())
+    e_st = float((st_out.float() - ref_out.float()).abs().mean())
+    print(f"[parity] swa mean |out - golden|: exact {e_ex:.4g}, streaming {e_st:.4g}", flush=True)
+    assert e_ex <= e_st
 
 
 def test_bsnd_layout_with_padding():
