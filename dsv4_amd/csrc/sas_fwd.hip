@@ -35,6 +35,8 @@
 
 #include "sas_kern.h"
 
+#include <mutex>
+
 #ifndef SAS_PFK
 #define SAS_PFK 3   // K operand k-steps read ahead (32-row steps)
 #endif
@@ -1402,6 +1404,78 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
                      : dispatch_hw<512, _Float16, 0>(pl.hw, pl.nw, pl.exact, fp, nblocks, st);
   if (rc || pl.nsplit == 1 || (a->flags & SAS_FWD_NO_COMBINE)) return rc;
   return launch_combine(fp, a->q_dtype, st);
+}
+
+// ---------------------------------------------------------------------------
+// no-allocation forward: split partials in a file-scope device array
+// ---------------------------------------------------------------------------
+
+namespace {
+
+constexpr size_t kScratchBytes = size_t(16) << 20;   // split partials of one call, at most
+constexpr int kMaxDevices = 64;
+
+// Each device holds its own copy once the library's code object is loaded
+// there. Host code never uses this name as an address: the device address
+// comes from hipGetSymbolAddress, once per device (scratch_ptr below).
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the stream's device, which must be the
+// current device; looked up on the first call per device.
+int scratch_ptr(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(SAS_ELAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (st) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(st, &sdev);
+    if (e != hipSuccess) return set_error(SAS_ELAUNCH, "hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (sdev != dev)
+      return set_error(SAS_EINVAL, "no-alloc forward: the stream is on device %d, the current device is %d",
+                       (int)sdev, dev);
+  }
+  if (dev < 0 || dev >= kMaxDevices) return set_error(SAS_EINVAL, "device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(SAS_ELAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SAS_OK;
+}
+
+}  // namespace
+
+extern "C" int sas_fwd_noalloc_v1(const SasFwdArgs* a, void* stream) {
+  sas::clear_error();
+  Plan pl;
+  const int rc = make_plan(a, &pl);
+  if (rc) return rc;
+  if (a->flags & SAS_FWD_NO_COMBINE)
+    return sas::set_error(SAS_EINVAL, "no-alloc forward: SAS_FWD_NO_COMBINE would leave the partials in the "
+                                      "library's scratch; use sas_fwd_v1 with a workspace");
+  if (pl.ws > kScratchBytes)
+    return sas::set_error(SAS_ENOWS, "no-alloc forward: %zu bytes of split partials needed, beyond the %zu-byte "
+                                     "scratch (use sas_fwd_v1 with a workspace, or fewer tokens per call)",
+                          pl.ws, kScratchBytes);
+  if (a->T == 0) return SAS_OK;
+  SasFwdArgs b = *a;
+  b.workspace = nullptr;
+  b.workspace_bytes = 0;
+  if (pl.ws) {
+    void* ptr = nullptr;
+    const int r2 = scratch_ptr((hipStream_t)stream, &ptr);
+    if (r2) return r2;
+    b.workspace = ptr;
+    b.workspace_bytes = kScratchBytes;
+  }
+  return sas_fwd_v1(&b, stream);
 }
 
 extern "C" int sas_combine_v1(const SasCombineArgs* a, void* stream) {

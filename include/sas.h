@@ -142,6 +142,20 @@ int sas_fwd_plan(const SasFwdArgs* a, int32_t* num_splits, size_t* workspace_byt
 int sas_fwd_v1(const SasFwdArgs* a, void* stream);
 
 /*
+ * sas_fwd_v1 without any allocation by caller or library, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The split partials go to a 16 MiB (16777216-byte) device array of the
+ * library (one per device, held until the process ends) instead of a caller
+ * workspace: `workspace` / `workspace_bytes` are ignored, and a call whose
+ * plan needs more (the workspace size sas_fwd_plan reports) fails with
+ * SAS_ENOWS. SAS_FWD_NO_COMBINE is rejected. `stream` must belong to the
+ * current device. Calls that overlap on one device share the array and race:
+ * serialise them (one stream, or events).
+ */
+int sas_fwd_noalloc_v1(const SasFwdArgs* a, void* stream);
+
+/*
  * Split-KV LSE combine (no counterpart launched by the reference: its
  * flash-decode fields stay zero, metadata.py:323-325): for each (token, head)
  * M = max(sink, m_i), L = e^(sink-M) + sum_i l_i e^(m_i-M),
