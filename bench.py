@@ -200,6 +200,27 @@ def pmc_pass():
     print("[pmc-pass] done", flush=True)
 
 
+def prefill_pass():
+    """Child of a `rocprofv3 --pmc` run for the MFMA counters of the C3
+    prefill kernel: a bf16 GEMM of known FLOP (8192^3, hipBLASLt) three
+    times, then the C3 forward five times."""
+    from dsv4_amd import cases
+    torch.cuda.init()
+    m = 8192
+    a = torch.randn(m, m, device="cuda").to(torch.bfloat16)
+    b = torch.randn(m, m, device="cuda").to(torch.bfloat16)
+    for _ in range(3):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    del a, b
+    inp = cases.make_inputs(cases.CONFIGS["C3"], device="cuda")
+    call = _prepare(inp)
+    for _ in range(5):
+        call.launch()
+    torch.cuda.synchronize()
+    print(f"[prefill-pass] done: {cases.gathered_rows(inp)} (token, key) pairs", flush=True)
+
+
 def _read_counter(outdir, counter):
     """{kernel substring: [per-dispatch values]} for the counter."""
     vals = {SPLIT_KERNEL: [], COMBINE_KERNEL: [], CAL_KERNEL: [], CW_KERNEL: []}
@@ -383,6 +404,7 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C4 / C5 decode lines")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured copy / GEMM peaks")
     ap.add_argument("--pmc-pass", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--prefill-pass", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this operator build runs on a single MI355X "
@@ -390,6 +412,9 @@ def main():
         sys.exit(2)
     if args.pmc_pass:
         pmc_pass()
+        return
+    if args.prefill_pass:
+        prefill_pass()
         return
 
     # counter passes run first, in child processes, before this process

@@ -69,6 +69,23 @@ def test_oracle_sink_gradient_closed_form():
 
 
 @pytest.mark.parametrize("scenario", [1, 2, 3])
+def test_oracle_given_forward_equals_autograd(scenario):
+    """The explicit FlashAttention-2 formulas from the exact forward's out /
+    lse give the autograd gradients (dq, touched cache rows, sinks); a
+    planted sign error in dS does not."""
+    q, dout, kw = _tiny(scenario=scenario, seed=10 + scenario)
+    r = BR.backward_paged(q, dout, **kw)
+    e = BR.backward_given_forward(q, dout, r["out"], r["lse"], **kw)
+    torch.testing.assert_close(e["dq"], r["dq"], atol=1e-10, rtol=1e-9)
+    torch.testing.assert_close(e["d_sinks"], r["d_sinks"], atol=1e-10, rtol=1e-9)
+    for key in ("d_ori", "d_cmp") if scenario >= 2 else ("d_ori",):
+        assert torch.equal(e[key][0], r[key][0])
+        torch.testing.assert_close(e[key][1], r[key][1], atol=1e-10, rtol=1e-9)
+    bad = BR.backward_given_forward(q, dout, r["out"], r["lse"], plant_sign=True, **kw)
+    assert not torch.allclose(bad["dq"], r["dq"], atol=1e-6, rtol=1e-6)
+
+
+@pytest.mark.parametrize("scenario", [1, 2, 3])
 def test_oracle_finite_differences(scenario):
     """Central differences of sum(dO * out) in fp64 match the autograd
     gradients of q, of cache rows (a V channel and a rope channel) and of the
@@ -184,10 +201,14 @@ def _check_against_oracle(name, inp, dq, d_ori, d_cmp, d_sinks, r):
     print(f"[bwd] {name}: worst err / bound = {worst}", flush=True)
 
 
-def _oracle_bwd(inp, dout, tokens=None):
+def _oracle_bwd(inp, dout, out, lse, tokens=None):
+    """The fp64 backward from the GPU forward's own out / lse (the inputs
+    sas_bwd_v1 takes; the formulas are pinned to autograd above): the GPU
+    result may then differ only by its bf16 operand roundings and fp32
+    accumulation, element by element."""
     c = inp.cfg
-    return BR.backward_paged(
-        inp.q, dout, ori_kv=inp.ori_kv, ori_block_table=inp.ori_bt, cu_seqlens_q=inp.cu_seqlens_q,
+    return BR.backward_given_forward(
+        inp.q, dout, out, lse, ori_kv=inp.ori_kv, ori_block_table=inp.ori_bt, cu_seqlens_q=inp.cu_seqlens_q,
         seqused_kv=inp.seqused_kv, sinks=inp.sinks, softmax_scale=c.scale,
         cmp_kv=inp.cmp_kv if c.scenario >= 2 else None, cmp_block_table=inp.cmp_bt if c.scenario >= 2 else None,
         cmp_sparse_indices=inp.cmp_idx if c.scenario == 3 else None, cmp_ratio=c.cmp_ratio,
@@ -209,7 +230,7 @@ def test_gpu_backward_matches_oracle(name):
     torch.cuda.synchronize()
     # tolerance: bf16 / fp16 rounding of the forward output (used in Delta),
     # of the MFMA operands dS / P and of dq; fp32 accumulation elsewhere
-    _check_against_oracle(name, inp, dq, d_ori, d_cmp, d_sinks, _oracle_bwd(inp, dout))
+    _check_against_oracle(name, inp, dq, d_ori, d_cmp, d_sinks, _oracle_bwd(inp, dout, out, lse))
 
 
 @pytest.mark.gpu
@@ -225,7 +246,7 @@ def test_gpu_backward_c2_decode_full():
     dout = torch.randn(out.shape, generator=g).to(inp.q.dtype)
     dq, d_ori, d_cmp, d_sinks = sparse_attn_sharedkv_backward(dout.cuda(), d.q, out, lse, **kw)
     torch.cuda.synchronize()
-    _check_against_oracle("C2", inp, dq, d_ori, d_cmp, d_sinks, _oracle_bwd(inp, dout))
+    _check_against_oracle("C2", inp, dq, d_ori, d_cmp, d_sinks, _oracle_bwd(inp, dout, out, lse))
 
 
 @pytest.mark.gpu
@@ -247,7 +268,7 @@ def test_gpu_backward_c3_prefill_sampled():
     dout[toks] = torch.randn((len(toks),) + tuple(out.shape[1:]), generator=g).to(inp.q.dtype)
     dq, d_ori, d_cmp, d_sinks = sparse_attn_sharedkv_backward(dout.cuda(), d.q, out, lse, **kw)
     torch.cuda.synchronize()
-    r = _oracle_bwd(inp, dout, tokens=toks)
+    r = _oracle_bwd(inp, dout, out, lse, tokens=toks)
     _check_against_oracle("C3 sampled", inp, dq, d_ori, d_cmp, d_sinks, r)
 
 
@@ -348,8 +369,4 @@ def test_gpu_backward_h48_d512_matches_oracle():
     dout = torch.randn(out.shape, generator=g).to(out.dtype)
     dq, d_ori, d_cmp, d_snk = sparse_attn_sharedkv_backward(dout.cuda(), d.q, out, lse, **kw)
     torch.cuda.synchronize()
-    r = BR.backward_paged(inp.q, dout, ori_kv=inp.ori_kv, ori_block_table=inp.ori_bt,
-                          cu_seqlens_q=inp.cu_seqlens_q, seqused_kv=inp.seqused_kv, sinks=inp.sinks,
-                          softmax_scale=c.scale, cmp_kv=inp.cmp_kv, cmp_block_table=inp.cmp_bt,
-                          cmp_sparse_indices=inp.cmp_idx, cmp_ratio=c.cmp_ratio, ori_win_left=c.win_left)
-    _check_against_oracle("h48_d512", inp, dq, d_ori, d_cmp, d_snk, r)
+    _check_against_oracle("h48_d512", inp, dq, d_ori, d_cmp, d_snk, _oracle_bwd(inp, dout, out, lse))
