@@ -14,15 +14,23 @@ the first 512 channels, so ``out`` is ``[..., 512]``); any top-k width; any
 block size; and an fp8 cache given as uint8 ``[num_blocks, block_size, 1,
 656]`` rows (see :mod:`dsv4_amd.paged`) with a bf16 query.
 
-``metadata`` is validated (int32, 1024 entries) and synthesised with the
-bit-exact scheduler when omitted (api.py:335-366). The GPU kernel does not
+``metadata`` is validated (int32, 1024 entries). The GPU kernel does not
 need it for scheduling: it launches one workgroup per (token, head group,
-KV split) and covers every valid token by construction.
+KV split) and covers every valid token by construction; an omitted one is
+built with the bit-exact scheduler on request (:meth:`PreparedCall.metadata`).
+
+Host cost of a call: the argument resolution (routing, checks, launch
+arguments, split plan) is cached per call signature (shapes, dtypes, device
+pointers, scalars, stream), so a repeated call allocates ``out`` / ``lse``,
+copies host-side sequence lengths through a reused pinned buffer, and
+launches. Device ``cu_seqlens_q`` is passed to the kernel as it is.
 """
 
 from __future__ import annotations
 
 import ctypes as C
+import threading
+from collections import OrderedDict
 from typing import Optional, Tuple, Union
 
 import torch
@@ -35,123 +43,98 @@ _DT = {torch.bfloat16: _lib.SAS_DT_BF16, torch.float16: _lib.SAS_DT_FP16}
 FP8_ROW_BYTES = 656
 
 
-def _dev_i32(t: torch.Tensor, device) -> torch.Tensor:
-    return t.to(device=device, dtype=torch.int32).contiguous()
+# ---------------------------------------------------------------------------
+# per-call helpers: pinned staging of host int32 arrays, workspaces
+# ---------------------------------------------------------------------------
+
+class _Staging:
+    """A ring of pinned host slots for the small int32 arrays a call copies
+    to the device (host-side sequence lengths), so no call pins memory. A
+    slot is reused only after the copy that last read it has completed."""
+
+    SLOTS, SLOT_INTS = 64, 8192
+
+    def __init__(self):
+        self.buf = torch.empty(self.SLOTS * self.SLOT_INTS, dtype=torch.int32, pin_memory=True)
+        self.events = [torch.cuda.Event() for _ in range(self.SLOTS)]
+        self.used = [False] * self.SLOTS
+        self.next = 0
+        self.lock = threading.Lock()
+
+    def to_device(self, parts, device, stream) -> torch.Tensor:
+        """Concatenation of ``parts`` (host int32 tensors) as a new device
+        tensor, copied on ``stream`` without blocking the host."""
+        n = sum(int(t.numel()) for t in parts)
+        if n > self.SLOT_INTS:
+            return torch.cat([t.reshape(-1) for t in parts]).to(device)
+        with self.lock:
+            slot = self.next
+            self.next = (slot + 1) % self.SLOTS
+            ev = self.events[slot]
+            if self.used[slot]:
+                ev.synchronize()
+            host = self.buf[slot * self.SLOT_INTS: slot * self.SLOT_INTS + n]
+            if len(parts) == 1:
+                host.copy_(parts[0].reshape(-1))
+            else:
+                torch.cat([t.reshape(-1) for t in parts], out=host)
+            dev = torch.empty(n, dtype=torch.int32, device=device)
+            if stream == torch.cuda.current_stream(device):
+                dev.copy_(host, non_blocking=True)
+            else:
+                with torch.cuda.stream(stream):
+                    dev.copy_(host, non_blocking=True)
+            ev.record(stream)
+            self.used[slot] = True
+        return dev
 
 
-class PreparedCall:
-    """Arguments of one forward, resolved and allocated; :meth:`launch` runs
-    the kernels on the current (or given) stream without host syncs."""
-
-    def __init__(self, args: _lib.SasFwdArgs, keep: list, out, lse, layout_q, B, S_max):
-        self.args = args
-        self._keep = keep
-        self.out = out
-        self.lse = lse
-        self.layout_q = layout_q
-        self.B = B
-        self.S_max = S_max
-        self._prep_stream = torch.cuda.current_stream(out.device)
-        ns = C.c_int32(0)
-        ws = C.c_size_t(0)
-        _lib.check(_lib.lib().sas_fwd_plan(C.byref(args), C.byref(ns), C.byref(ws)),
-                   "sparse_attn_sharedkv")
-        self.num_splits = ns.value
-        self.workspace = None
-        if ws.value:
-            self.workspace = torch.empty(ws.value, dtype=torch.uint8, device=out.device)
-            args.workspace = self.workspace.data_ptr()
-            args.workspace_bytes = ws.value
-        args.num_splits = self.num_splits
-
-    def _stream(self, stream):
-        st = stream if stream is not None else torch.cuda.current_stream(self.out.device)
-        if st != self._prep_stream:
-            # the device-side offsets and copies were enqueued on the stream
-            # that was current when the call was prepared
-            ev = torch.cuda.Event()
-            ev.record(self._prep_stream)
-            st.wait_event(ev)
-        return C.c_void_p(st.cuda_stream)
-
-    def launch(self, stream: Optional[torch.cuda.Stream] = None) -> None:
-        """Split kernel, then (with more than one split) the LSE combine."""
-        self.args.flags = 0
-        _lib.check(_lib.lib().sas_fwd_v1(C.byref(self.args), self._stream(stream)),
-                   "sparse_attn_sharedkv")
-
-    def launch_split(self, stream: Optional[torch.cuda.Stream] = None) -> None:
-        """Split kernel only; with more than one split the result is the fp32
-        partials in :attr:`workspace` until :meth:`launch_combine` runs."""
-        self.args.flags = _lib.SAS_FWD_NO_COMBINE
-        try:
-            _lib.check(_lib.lib().sas_fwd_v1(C.byref(self.args), self._stream(stream)),
-                       "sparse_attn_sharedkv")
-        finally:
-            self.args.flags = 0
-
-    def combine_args(self) -> _lib.SasCombineArgs:
-        a = self.args
-        ca = _lib.SasCombineArgs()
-        ca.part_o = a.workspace
-        pb = 4 if a.q_dtype == _lib.SAS_DT_FP16 else 2   # part_o element: fp32 under fp16 out, else fp16
-        ca.part_ml = a.workspace + a.T * self.num_splits * a.H * a.DV * pb
-        ca.sinks, ca.out, ca.lse = a.sinks, a.out, a.lse
-        ca.T, ca.S, ca.H, ca.DV = a.T, self.num_splits, a.H, a.DV
-        ca.out_dtype = a.q_dtype
-        return ca
-
-    def launch_combine(self, stream: Optional[torch.cuda.Stream] = None) -> None:
-        """LSE combine of the partials left by :meth:`launch_split`."""
-        if self.num_splits <= 1:
-            return
-        ca = self.combine_args()
-        _lib.check(_lib.lib().sas_combine_v1(C.byref(ca), self._stream(stream)),
-                   "sparse_attn_sharedkv combine")
-
-    def metadata(self) -> torch.Tensor:
-        """The reference's int32[1024] scheduler metadata for this call: the
-        tensor passed in, else synthesised with the bit-exact scheduler
-        (metadata.py:258-1086). The kernels do not need it."""
-        return self._metadata_fn()
-
-    def result(self, return_softmax_lse: bool):
-        out, lse = self.out, self.lse
-        if self.layout_q == "BSND":
-            out = out.reshape(self.B, self.S_max, out.shape[1], out.shape[2])
-            lse = lse.reshape(self.B, self.S_max, lse.shape[1])
-        return (out, lse) if return_softmax_lse else out
+_staging = None
+_staging_lock = threading.Lock()
 
 
-def prepare_sparse_attn_sharedkv(
-    q: torch.Tensor,
-    *,
-    ori_kv: torch.Tensor,
-    cmp_kv: Optional[torch.Tensor] = None,
-    cmp_sparse_indices: Optional[torch.Tensor] = None,
-    ori_block_table: torch.Tensor,
-    cmp_block_table: Optional[torch.Tensor] = None,
-    cu_seqlens_q: Optional[torch.Tensor] = None,
-    seqused_q: Optional[torch.Tensor] = None,
-    seqused_kv: torch.Tensor,
-    sinks: torch.Tensor,
-    metadata: Optional[torch.Tensor] = None,
-    softmax_scale: float,
-    cmp_ratio: Optional[int] = None,
-    ori_mask_mode: int = 4,
-    cmp_mask_mode: int = 3,
-    ori_win_left: int = 127,
-    ori_win_right: int = 0,
-    layout_q: str = "TND",
-    layout_kv: str = "PA_ND",
-    core_num: int = DEFAULT_CORE_NUM,
-    topk_cmp: Optional[int] = None,
-    num_splits: int = 0,
-    head_waves: int = 0,
-    waves: int = 0,
-) -> PreparedCall:
-    """Validate and resolve the arguments of :func:`sparse_attn_sharedkv`
-    (api.py:186-366) and allocate outputs; see that function."""
+def _stage(parts, device, stream) -> torch.Tensor:
+    global _staging
+    if _staging is None:
+        with _staging_lock:
+            if _staging is None:
+                _staging = _Staging()
+    return _staging.to_device(parts, device, stream)
+
+
+# split-KV workspaces, one growing buffer per (device, stream): the calls of
+# one stream run in order, so they can share it
+_workspaces = {}
+_ws_lock = threading.Lock()
+
+
+def _workspace(device, stream, nbytes: int) -> torch.Tensor:
+    key = (device, stream.cuda_stream)
+    with _ws_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            with torch.cuda.stream(stream):
+                ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+    return ws
+
+
+# ---------------------------------------------------------------------------
+# argument resolution (api.py:186-366)
+# ---------------------------------------------------------------------------
+
+class _Resolved:
+    """A call's launch arguments with everything except its outputs, its
+    workspace and host-side sequence lengths (staged per call)."""
+
+    __slots__ = ("args", "keep", "device", "dtype", "T1", "N1", "layout_q", "B", "S_max", "host_parts",
+                 "num_splits", "ws_bytes", "cacheable", "metadata_fn")
+
+
+def _resolve(q, *, ori_kv, cmp_kv, cmp_sparse_indices, ori_block_table, cmp_block_table, cu_seqlens_q,
+             seqused_q, seqused_kv, sinks, metadata, softmax_scale, cmp_ratio, ori_mask_mode, cmp_mask_mode,
+             ori_win_left, ori_win_right, layout_q, layout_kv, core_num, topk_cmp, num_splits, head_waves,
+             waves) -> _Resolved:
     del seqused_q  # API-parity placeholder, as in the reference (api.py:186)
     assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
     assert cmp_mask_mode == 3 or cmp_kv is None, "only cmp_mask_mode=3 supported"
@@ -163,29 +146,24 @@ def prepare_sparse_attn_sharedkv(
     if not q.is_cuda:
         raise ValueError("sparse_attn_sharedkv runs on the GPU: q must be a device tensor")
     dev = q.device
+    r = _Resolved()
+    r.cacheable = True
 
     scenario = _lib.SAS_SWA if cmp_kv is None else (
         _lib.SAS_CFA if cmp_sparse_indices is None else _lib.SAS_SCFA)
 
     # ---- flat [total_tokens, N1, D] view + per-batch token offsets ----------
-    # q_prefix / act_q (int32 [B]) reach the kernel as device arrays. With a
-    # device cu_seqlens_q they are computed on the device (no host sync); host
-    # values are copied through pinned memory without blocking.
-    dev_cu = None
+    # TND: the kernel takes cu_seqlens_q itself (q_prefix = cu_seqlens_q,
+    # act_q = NULL), on the device as given or copied there per call.
+    # BSND: q_prefix = b * S_max and the lengths, copied per call.
     if layout_q == "TND":
         assert cu_seqlens_q is not None, "cu_seqlens_q is required for TND"
         B = cu_seqlens_q.numel() - 1
         S_max = None   # not needed for TND outputs
         T1, N1, D = q.shape
         q_flat = q
-        if cu_seqlens_q.is_cuda:
-            dev_cu = cu_seqlens_q.to(device=dev, dtype=torch.int32).contiguous()
-            q_prefix = act_q = None
-        else:
-            cu = cu_seqlens_q.to(torch.int32)
-            q_prefix = cu[:-1]
-            act_q = cu[1:] - cu[:-1]
         idx_flat = cmp_sparse_indices if scenario == _lib.SAS_SCFA else None
+        seq_parts = [("cu", cu_seqlens_q)]
     else:
         B, S_max, N1, D = q.shape
         T1 = B * S_max
@@ -200,6 +178,8 @@ def prepare_sparse_attn_sharedkv(
         if scenario == _lib.SAS_SCFA:
             ci = cmp_sparse_indices
             idx_flat = ci.reshape(T1, ci.shape[2], ci.shape[3])
+        seq_parts = [("qp", q_prefix), ("aq", act_q)]
+        r.cacheable = False
     if B < 1:
         raise ValueError("batch must be at least 1")
 
@@ -215,6 +195,7 @@ def prepare_sparse_attn_sharedkv(
         N2 = cmp_kv.shape[2]
         if cmp_ratio is None:
             cmp_ratio = 4
+        # api.py:259-261: the slot count follows the longest sequence
         K = int(seqused_kv.max().item()) // cmp_ratio if seqused_kv.numel() else 0
     else:
         N2 = ori_kv.shape[2]
@@ -233,6 +214,8 @@ def prepare_sparse_attn_sharedkv(
     cmp_ratio_eff = cmp_ratio if cmp_ratio is not None else 4
     if scenario >= _lib.SAS_CFA and cmp_ratio_eff < 1:
         raise ValueError("cmp_ratio must be >= 1")
+    if seqused_kv.numel() != B:
+        raise ValueError(f"seqused_kv has {seqused_kv.numel()} entries, batch is {B}")
 
     # ---- metadata (api.py:335-366) -------------------------------------------
     # A given tensor is validated. The kernel covers every (token, head group,
@@ -267,11 +250,17 @@ def prepare_sparse_attn_sharedkv(
         return sparse_attn_sharedkv_metadata(**meta_kwargs)
 
     # ---- device operands ------------------------------------------------------
+    # Used as given when already int32 / contiguous on the device; otherwise
+    # converted (kept alive with the call, which is then not cached: the
+    # converted copies are new tensors each time).
     keep = []
 
     def d(t, dtype=None):
         if t is None:
             return None
+        if t.device == dev and (dtype is None or t.dtype == dtype) and t.is_contiguous():
+            return t
+        r.cacheable = False
         t = t.to(device=dev, dtype=dtype) if dtype is not None else t.to(device=dev)
         t = t.contiguous()
         keep.append(t)
@@ -283,37 +272,31 @@ def prepare_sparse_attn_sharedkv(
     ckv = d(cmp_kv) if scenario >= _lib.SAS_CFA else None
     cbt = d(cmp_block_table, torch.int32) if scenario >= _lib.SAS_CFA else None
     cidx = d(idx_flat, torch.int32) if scenario == _lib.SAS_SCFA else None
-    if seqused_kv.numel() != B:
-        raise ValueError(f"seqused_kv has {seqused_kv.numel()} entries, batch is {B}")
-    if dev_cu is not None:
-        qp_d = dev_cu[:-1]
-        aq_d = dev_cu[1:] - dev_cu[:-1]
-        keep.extend([dev_cu, aq_d])
-    else:
-        # one pinned staging buffer, copied without blocking the host
-        hb = torch.cat([q_prefix.to(torch.int32), act_q.to(torch.int32)]).pin_memory()
-        hd = hb.to(device=dev, non_blocking=True)
-        keep.extend([hb, hd])
-        qp_d, aq_d = hd[:B], hd[B:]
-    if seqused_kv.is_cuda:
-        akv_d = d(seqused_kv.reshape(-1), torch.int32)
-    else:
-        kb = seqused_kv.to(torch.int32).reshape(-1).contiguous().pin_memory()
-        akv_d = kb.to(device=dev, non_blocking=True)
-        keep.extend([kb, akv_d])
     snk = d(sinks, torch.float32)
     if snk.numel() != N1:
         raise ValueError(f"sinks must have {N1} entries (got {snk.numel()})")
-    out = torch.empty((T1, N1, 512), dtype=q.dtype, device=dev)
-    lse = torch.empty((T1, N1), dtype=torch.float32, device=dev)
 
     a = _lib.SasFwdArgs()
+    host_parts = []
+    for name, t in seq_parts + [("kv", seqused_kv.reshape(-1))]:
+        if t.is_cuda:
+            td = d(t, torch.int32)
+            if name == "cu":
+                a.q_prefix, a.act_q = td.data_ptr(), None
+            elif name == "qp":
+                a.q_prefix = td.data_ptr()
+            elif name == "aq":
+                a.act_q = td.data_ptr()
+            else:
+                a.act_kv = td.data_ptr()
+        else:
+            host_parts.append((name, t.to(torch.int32).reshape(-1)))
+
     a.q, a.ori_kv, a.ori_block_table = qd.data_ptr(), okv.data_ptr(), obt.data_ptr()
     a.cmp_kv = ckv.data_ptr() if ckv is not None else None
     a.cmp_block_table = cbt.data_ptr() if cbt is not None else None
     a.cmp_indices = cidx.data_ptr() if cidx is not None else None
-    a.q_prefix, a.act_q, a.act_kv = qp_d.data_ptr(), aq_d.data_ptr(), akv_d.data_ptr()
-    a.sinks, a.out, a.lse = snk.data_ptr(), out.data_ptr(), lse.data_ptr()
+    a.sinks = snk.data_ptr()
     a.T, a.B, a.H, a.D, a.DV = T1, B, N1, D, 512
     a.ori_block_size, a.ori_bt_stride, a.ori_num_blocks = okv.shape[1], obt.shape[1], okv.shape[0]
     if ckv is not None:
@@ -328,9 +311,188 @@ def prepare_sparse_attn_sharedkv(
     a.num_splits = int(num_splits)
     a.head_waves = int(head_waves)
     a.waves = int(waves)
-    call = PreparedCall(a, keep, out, lse, layout_q, B, S_max)
-    call._metadata_fn = _metadata
-    return call
+    ns = C.c_int32(0)
+    ws = C.c_size_t(0)
+    _lib.check(_lib.lib().sas_fwd_plan(C.byref(a), C.byref(ns), C.byref(ws)), "sparse_attn_sharedkv")
+    a.num_splits = ns.value
+    r.args, r.keep, r.device, r.dtype = a, keep, dev, q.dtype
+    r.T1, r.N1, r.layout_q, r.B, r.S_max = T1, N1, layout_q, B, S_max
+    r.host_parts = host_parts
+    r.num_splits, r.ws_bytes = ns.value, ws.value
+    r.metadata_fn = _metadata
+    return r
+
+
+def _bind_seqlens(r: _Resolved, parts, a: _lib.SasFwdArgs, stream, keep: list) -> None:
+    """Copy the call's host-side sequence lengths ``parts`` ((name, int32
+    tensor) pairs, the names of ``r.host_parts``) to the device through the
+    pinned ring and point the launch arguments at them."""
+    if not parts:
+        return
+    dev = _stage([t for _, t in parts], r.device, stream)
+    keep.append(dev)
+    o = 0
+    base = dev.data_ptr()
+    for name, t in parts:
+        ptr = base + 4 * o
+        if name == "cu":
+            a.q_prefix, a.act_q = ptr, None
+        elif name == "qp":
+            a.q_prefix = ptr
+        elif name == "aq":
+            a.act_q = ptr
+        else:
+            a.act_kv = ptr
+        o += int(t.numel())
+
+
+class PreparedCall:
+    """Arguments of one forward, resolved and allocated; :meth:`launch` runs
+    the kernels on the current (or given) stream without host syncs."""
+
+    def __init__(self, r: _Resolved):
+        self._r = r
+        dev = r.device
+        self.out = torch.empty((r.T1, r.N1, 512), dtype=r.dtype, device=dev)
+        self.lse = torch.empty((r.T1, r.N1), dtype=torch.float32, device=dev)
+        self.layout_q, self.B, self.S_max = r.layout_q, r.B, r.S_max
+        self.num_splits = r.num_splits
+        self._prep_stream = torch.cuda.current_stream(dev)
+        self._keep = list(r.keep)
+        self.args = _lib.SasFwdArgs.from_buffer_copy(r.args)
+        self.args.out, self.args.lse = self.out.data_ptr(), self.lse.data_ptr()
+        _bind_seqlens(r, r.host_parts, self.args, self._prep_stream, self._keep)
+        self.workspace = None
+        if r.ws_bytes:
+            self.workspace = torch.empty(r.ws_bytes, dtype=torch.uint8, device=dev)
+            self.args.workspace = self.workspace.data_ptr()
+            self.args.workspace_bytes = r.ws_bytes
+
+    def _stream(self, stream):
+        st = stream if stream is not None else torch.cuda.current_stream(self.out.device)
+        if st != self._prep_stream:
+            # the device-side copies were enqueued on the stream that was
+            # current when the call was prepared
+            ev = torch.cuda.Event()
+            ev.record(self._prep_stream)
+            st.wait_event(ev)
+        return C.c_void_p(st.cuda_stream)
+
+    def launch(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Split kernel, then (with more than one split) the LSE combine."""
+        self.args.flags = 0
+        _lib.check(_lib.lib().sas_fwd_v1(C.byref(self.args), self._stream(stream)),
+                   "sparse_attn_sharedkv")
+
+    def launch_split(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Split kernel only; with more than one split the result is the
+        partials in :attr:`workspace` until :meth:`launch_combine` runs."""
+        self.args.flags = _lib.SAS_FWD_NO_COMBINE
+        try:
+            _lib.check(_lib.lib().sas_fwd_v1(C.byref(self.args), self._stream(stream)),
+                       "sparse_attn_sharedkv")
+        finally:
+            self.args.flags = 0
+
+    def combine_args(self) -> _lib.SasCombineArgs:
+        a = self.args
+        ca = _lib.SasCombineArgs()
+        ca.part_o = a.workspace
+        pb = 4 if a.q_dtype == _lib.SAS_DT_FP16 else 2   # part_o element: fp32 under fp16 out, else fp16
+        ca.part_ml = a.workspace + a.T * self.num_splits * a.H * a.DV * pb
+        ca.sinks, ca.out, ca.lse = a.sinks, a.out, a.lse
+        ca.T, ca.S, ca.H, ca.DV = a.T, self.num_splits, a.H, a.DV
+        ca.out_dtype = a.q_dtype
+        return ca
+
+    def launch_combine(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+        """LSE combine of the partials left by :meth:`launch_split`."""
+        if self.num_splits <= 1:
+            return
+        ca = self.combine_args()
+        _lib.check(_lib.lib().sas_combine_v1(C.byref(ca), self._stream(stream)),
+                   "sparse_attn_sharedkv combine")
+
+    def metadata(self) -> torch.Tensor:
+        """The reference's int32[1024] scheduler metadata for this call: the
+        tensor passed in, else synthesised with the bit-exact scheduler
+        (metadata.py:258-1086). The kernels do not need it."""
+        return self._r.metadata_fn()
+
+    def result(self, return_softmax_lse: bool):
+        return _result(self.out, self.lse, self.layout_q, self.B, self.S_max, return_softmax_lse)
+
+
+def _result(out, lse, layout_q, B, S_max, return_softmax_lse):
+    if layout_q == "BSND":
+        out = out.reshape(B, S_max, out.shape[1], out.shape[2])
+        lse = lse.reshape(B, S_max, lse.shape[1])
+    return (out, lse) if return_softmax_lse else out
+
+
+_FWD_DEFAULTS = dict(cmp_kv=None, cmp_sparse_indices=None, cmp_block_table=None, cu_seqlens_q=None,
+                     seqused_q=None, metadata=None, cmp_ratio=None, ori_mask_mode=4, cmp_mask_mode=3,
+                     ori_win_left=127, ori_win_right=0, layout_q="TND", layout_kv="PA_ND",
+                     core_num=DEFAULT_CORE_NUM, topk_cmp=None, num_splits=0, head_waves=0, waves=0)
+
+
+def prepare_sparse_attn_sharedkv(
+    q: torch.Tensor,
+    *,
+    ori_kv: torch.Tensor,
+    cmp_kv: Optional[torch.Tensor] = None,
+    cmp_sparse_indices: Optional[torch.Tensor] = None,
+    ori_block_table: torch.Tensor,
+    cmp_block_table: Optional[torch.Tensor] = None,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    seqused_q: Optional[torch.Tensor] = None,
+    seqused_kv: torch.Tensor,
+    sinks: torch.Tensor,
+    metadata: Optional[torch.Tensor] = None,
+    softmax_scale: float,
+    cmp_ratio: Optional[int] = None,
+    ori_mask_mode: int = 4,
+    cmp_mask_mode: int = 3,
+    ori_win_left: int = 127,
+    ori_win_right: int = 0,
+    layout_q: str = "TND",
+    layout_kv: str = "PA_ND",
+    core_num: int = DEFAULT_CORE_NUM,
+    topk_cmp: Optional[int] = None,
+    num_splits: int = 0,
+    head_waves: int = 0,
+    waves: int = 0,
+) -> PreparedCall:
+    """Validate and resolve the arguments of :func:`sparse_attn_sharedkv`
+    (api.py:186-366) and allocate outputs and workspace; see that function."""
+    r = _resolve(q, ori_kv=ori_kv, cmp_kv=cmp_kv, cmp_sparse_indices=cmp_sparse_indices,
+                 ori_block_table=ori_block_table, cmp_block_table=cmp_block_table,
+                 cu_seqlens_q=cu_seqlens_q, seqused_q=seqused_q, seqused_kv=seqused_kv, sinks=sinks,
+                 metadata=metadata, softmax_scale=softmax_scale, cmp_ratio=cmp_ratio,
+                 ori_mask_mode=ori_mask_mode, cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
+                 ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv, core_num=core_num,
+                 topk_cmp=topk_cmp, num_splits=num_splits, head_waves=head_waves, waves=waves)
+    return PreparedCall(r)
+
+
+# ---------------------------------------------------------------------------
+# the drop-in entry point, with its per-signature cache
+# ---------------------------------------------------------------------------
+
+_CACHE_MAX = 64
+_cache: "OrderedDict[tuple, _Resolved]" = OrderedDict()
+_cache_lock = threading.Lock()
+
+
+def _sig(t):
+    """What a launch depends on for a tensor: device tensors by address and
+    geometry (their values are read by the kernel), host tensors by geometry
+    (their values are copied per call)."""
+    if t is None:
+        return None
+    if t.is_cuda:
+        return (t.data_ptr(), t.shape, t.stride(), t.dtype, t.device.index)
+    return ("host", t.shape, t.dtype)
 
 
 def sparse_attn_sharedkv(
@@ -365,16 +527,55 @@ def sparse_attn_sharedkv(
     (BSND) in q's dtype; ``lse`` is fp32 ``[T1, N1]`` / ``[B, S1, N1]`` with
     ``lse = max + ln(sum)`` over all attended keys and the sink.
     """
-    call = prepare_sparse_attn_sharedkv(
-        q, ori_kv=ori_kv, cmp_kv=cmp_kv, cmp_sparse_indices=cmp_sparse_indices,
-        ori_block_table=ori_block_table, cmp_block_table=cmp_block_table,
-        cu_seqlens_q=cu_seqlens_q, seqused_q=seqused_q, seqused_kv=seqused_kv, sinks=sinks,
-        metadata=metadata, softmax_scale=softmax_scale, cmp_ratio=cmp_ratio,
-        ori_mask_mode=ori_mask_mode, cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
-        ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
-        core_num=core_num, topk_cmp=topk_cmp)
-    call.launch()
-    return call.result(return_softmax_lse)
+    dev = q.device
+    stream = torch.cuda.current_stream(dev) if q.is_cuda else None
+    # CFA's slot count follows the longest sequence (api.py:259-261): part of
+    # the signature, read from the host copy, or through a sync as the
+    # reference does for device lengths
+    cfa_k = None
+    if cmp_kv is not None and cmp_sparse_indices is None and seqused_kv.numel():
+        cfa_k = int(seqused_kv.max().item())
+    key = (_sig(q), _sig(ori_kv), _sig(cmp_kv), _sig(cmp_sparse_indices), _sig(ori_block_table),
+           _sig(cmp_block_table), _sig(cu_seqlens_q), _sig(seqused_kv), _sig(sinks),
+           None if metadata is None else metadata.numel(), float(softmax_scale), cmp_ratio, ori_mask_mode,
+           cmp_mask_mode, ori_win_left, ori_win_right, layout_q, layout_kv, core_num, topk_cmp, cfa_k,
+           None if stream is None else stream.cuda_stream)
+    with _cache_lock:
+        r = _cache.get(key)
+        if r is not None:
+            _cache.move_to_end(key)
+    hit = r is not None
+    if not hit:
+        r = _resolve(q, ori_kv=ori_kv, cmp_kv=cmp_kv, cmp_sparse_indices=cmp_sparse_indices,
+                     ori_block_table=ori_block_table, cmp_block_table=cmp_block_table,
+                     cu_seqlens_q=cu_seqlens_q, seqused_q=seqused_q, seqused_kv=seqused_kv, sinks=sinks,
+                     metadata=metadata, softmax_scale=softmax_scale, cmp_ratio=cmp_ratio,
+                     ori_mask_mode=ori_mask_mode, cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
+                     ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
+                     core_num=core_num, topk_cmp=topk_cmp, num_splits=0, head_waves=0, waves=0)
+        if r.cacheable:
+            with _cache_lock:
+                _cache[key] = r
+                if len(_cache) > _CACHE_MAX:
+                    _cache.popitem(last=False)
+    out = torch.empty((r.T1, r.N1, 512), dtype=r.dtype, device=dev)
+    lse = torch.empty((r.T1, r.N1), dtype=torch.float32, device=dev)
+    a = _lib.SasFwdArgs.from_buffer_copy(r.args)
+    a.out, a.lse = out.data_ptr(), lse.data_ptr()
+    keep = []
+    if r.host_parts:
+        parts = r.host_parts
+        if hit:
+            # this call's host lengths (a cached resolution, TND only, holds
+            # an earlier call's)
+            cur = {"cu": cu_seqlens_q, "kv": seqused_kv}
+            parts = [(name, cur[name].to(torch.int32).reshape(-1)) for name, _ in r.host_parts]
+        _bind_seqlens(r, parts, a, stream, keep)
+    if r.ws_bytes:
+        ws = _workspace(dev, stream, r.ws_bytes)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), r.ws_bytes
+    _lib.check(_lib.lib().sas_fwd_v1(C.byref(a), C.c_void_p(stream.cuda_stream)), "sparse_attn_sharedkv")
+    return _result(out, lse, r.layout_q, r.B, r.S_max, return_softmax_lse)
 
 
 class PreparedBackward:

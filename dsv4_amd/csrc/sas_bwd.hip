@@ -327,7 +327,7 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   if (a->scenario >= SAS_CFA && (a->cmp_ratio < 1 || a->K < 0)) return set_error(SAS_EINVAL, "bwd: bad cmp_ratio/K");
   const long long nslots = a->win_left + 1 + (a->scenario >= SAS_CFA ? a->K : 0);
   if (a->T == 0) return SAS_OK;
-  if (!a->q || !a->ori_kv || !a->ori_block_table || !a->q_prefix || !a->act_q || !a->act_kv || !a->sinks ||
+  if (!a->q || !a->ori_kv || !a->ori_block_table || !a->q_prefix || !a->act_kv || !a->sinks ||
       !a->out || !a->lse || !ba->dout || !ba->dq || !ba->d_ori_kv || !ba->d_sinks)
     return set_error(SAS_EINVAL, "bwd: null device pointer");
   if (a->scenario >= SAS_CFA && (!a->cmp_kv || !a->cmp_block_table || !ba->d_cmp_kv))

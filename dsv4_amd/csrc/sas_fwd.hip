@@ -235,11 +235,7 @@ struct Fwd {
         const uint32_t w[4] = {fbuf[k].x, fbuf[k].y, fbuf[k].z, fbuf[k].w};
         uint32_t o[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t b0 = (w[i >> 1] >> ((i & 1) * 16)) & 0xffu;
-          const uint32_t b1 = (w[i >> 1] >> ((i & 1) * 16 + 8)) & 0xffu;
-          o[i] = pack2<__bf16>(e4m3_to_f32(b0) * fsc[k], e4m3_to_f32(b1) * fsc[k]);
-        }
+        for (int i = 0; i < 4; ++i) e4m3x4_to_bf16(w[i], fsc[k], o[2 * i], o[2 * i + 1]);
         row[(2 * c) ^ sw] = make_uint4(o[0], o[1], o[2], o[3]);
         row[(2 * c + 1) ^ sw] = make_uint4(o[4], o[5], o[6], o[7]);
       } else {
@@ -535,13 +531,7 @@ struct Fwd {
       // finished step it - 1, so its slot (J + NST - 1) % NST takes step
       // it + NST - 1 while step it computes.
       const int after = it < nsteps ? min(C::NST - 2, nsteps - 1 - it) : 0;
-      if constexpr (C::NI % C::WK) {
-        wait_vm_rt(max(after, 0) * nops);
-      } else {
-        if (after <= 0) wait_vm<0>();
-        else if (after == 1) wait_vm<C::OPS>();
-        else wait_vm<(C::NST > 3 ? 2 * C::OPS : 0)>();
-      }
+      wait_steps(after);
       step_sync();
       if (it < nsteps || C::QS) {
         const bool more = it + C::NST - 1 < nsteps;
@@ -565,13 +555,22 @@ struct Fwd {
   // slot that step it - 1 freed. Steps up to it + 2 have been issued when
   // iteration it starts.
   static constexpr bool kPipe = !KVF && C::NST == 4 && C::KW == 1 && NW == 4;
-  __device__ __forceinline__ void wait_steps(int n) {   // my DMAs of all but the n newest steps
+  // My DMAs of all but the n newest steps (n <= NST - 2) have landed. A wave
+  // issues OPS or OPS - 1 instructions per step (nops, wave-uniform), so the
+  // vmcnt immediate is one of a few compile-time values.
+  template <int M>
+  __device__ __forceinline__ void wait_ops(int n) {
+    static_assert(2 * M < 64, "vmcnt range");
+    if (n <= 0) wait_vm<0>();
+    else if (n == 1 || C::NST <= 3) wait_vm<M>();
+    else wait_vm<2 * M>();
+  }
+  __device__ __forceinline__ void wait_steps(int n) {
     if constexpr (C::NI % C::WK) {
-      wait_vm_rt(n * nops);
+      if (nops == C::OPS) wait_ops<C::OPS>(n);
+      else wait_ops<C::OPS - 1>(n);
     } else {
-      if (n <= 0) wait_vm<0>();
-      else if (n == 1) wait_vm<C::OPS>();
-      else wait_vm<2 * C::OPS>();
+      wait_ops<C::OPS>(n);
     }
   }
   template <int J>
@@ -877,7 +876,10 @@ template <int HW, int NW, int D, typename QT, int KVF, bool EXW>
 __global__ void __launch_bounds__(NW * 64)
 sas_fwd_kernel(const FwdParams p) {
   using C = Cfg<HW, NW, D, QT, KVF>;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // the wave index and every count derived from it are wave-uniform: kept
+  // in scalar registers, the step loop's bounds and DMA guards become scalar
+  // branches instead of exec-mask updates
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int item = item_index(p);
   if (item < 0) return;
   Tok k = item_of(p, item);
@@ -901,7 +903,7 @@ sas_fwd_kernel(const FwdParams p) {
         f.qf[n][ks] = qp[(long long)dh * (D / 8) + ((C::QS ? f.cs * C::KSQ : 0) + ks) * 4 + f.g];
     }
   });
-  const int nvalid = k.nvalid;
+  const int nvalid = __builtin_amdgcn_readfirstlane(k.nvalid);
 
   // key-group shares: whole steps, group 0 first
   const int per = ((nvalid + C::KW * C::TR - 1) / (C::KW * C::TR)) * C::TR;
@@ -1003,14 +1005,9 @@ struct Dec {
     } else {
       if (ks >= 16) return st.k[ks - 16];
       const float sc = ks < 4 ? st.sc.x : ks < 8 ? st.sc.y : ks < 12 ? st.sc.z : st.sc.w;
-      const uint32_t w[2] = {st.l8[ks].x, st.l8[ks].y};
       uint32_t o[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t b0 = (w[i >> 1] >> ((i & 1) * 16)) & 0xffu;
-        const uint32_t b1 = (w[i >> 1] >> ((i & 1) * 16 + 8)) & 0xffu;
-        o[i] = pack2<__bf16>(e4m3_to_f32(b0) * sc, e4m3_to_f32(b1) * sc);
-      }
+      e4m3x4_to_bf16(st.l8[ks].x, sc, o[0], o[1]);
+      e4m3x4_to_bf16(st.l8[ks].y, sc, o[2], o[3]);
       return make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
@@ -1113,13 +1110,16 @@ template <int D, typename QT, int KVF>
 __global__ void __launch_bounds__(256)
 sas_dec_kernel(const FwdParams p) {
   using C = Dec<D, QT, KVF>;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // the wave index and every count derived from it are wave-uniform: kept
+  // in scalar registers, the step loop's bounds and DMA guards become scalar
+  // branches instead of exec-mask updates
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int item = item_index(p);
   if (item < 0) return;
   Tok k = item_of(p, item);
   C f(p, lane);
   resolve<256, C::ROWB>(p, k, tid, lane, wave, [] {});
-  const int nvalid = k.nvalid;
+  const int nvalid = __builtin_amdgcn_readfirstlane(k.nvalid);
   const int hq = k.hg * 16 + f.c16;
   // key-group share of wave `wave`: whole 16-row steps, wave 0 first
   const int per = ((nvalid + 63) >> 6) << 4;
@@ -1281,9 +1281,11 @@ int dispatch_hw(int hw, int nw, bool exact, const FwdParams& fp, int nb, hipStre
   }
   if (hw == 1) return launch_dec<D, QT, KVF>(fp, nb, st);
   if (hw == 2 && nw == 4) return launch_fwd<2, 4, D, QT, KVF>(fp, nb, st);
-  if (hw == 2 && nw == 8) return launch_fwd<2, 8, D, QT, KVF>(fp, nb, st);
   if (hw == 4 && nw == 4) return launch_fwd<4, 4, D, QT, KVF>(fp, nb, st);
-  if (hw == 4 && nw == 8) return launch_fwd<4, 8, D, QT, KVF>(fp, nb, st);
+  if constexpr (!KVF) {   // fp8 rows are staged through registers: 4 waves only (make_plan)
+    if (hw == 2 && nw == 8) return launch_fwd<2, 8, D, QT, KVF>(fp, nb, st);
+    if (hw == 4 && nw == 8) return launch_fwd<4, 8, D, QT, KVF>(fp, nb, st);
+  }
   return sas::set_error(SAS_EINVAL, "unsupported head grouping");
 }
 
@@ -1335,7 +1337,7 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   int rc = make_plan(a, &pl);
   if (rc) return rc;
   if (a->T == 0) return SAS_OK;
-  if (!a->q || !a->ori_kv || !a->ori_block_table || !a->q_prefix || !a->act_q || !a->act_kv ||
+  if (!a->q || !a->ori_kv || !a->ori_block_table || !a->q_prefix || !a->act_kv ||
       !a->sinks || !a->out || !a->lse)
     return sas::set_error(SAS_EINVAL, "null device pointer");
   if (a->scenario >= SAS_CFA && (!a->cmp_kv || !a->cmp_block_table))

@@ -52,7 +52,7 @@ struct FwdParams {
   const int32_t* cmp_bt;
   const int32_t* cmp_idx;
   const int32_t* q_prefix;
-  const int32_t* act_q;
+  const int32_t* act_q;   // NULL: q_prefix holds B + 1 entries (cu_seqlens_q)
   const int32_t* act_kv;
   const float* sinks;
   uint8_t* out;
@@ -82,12 +82,16 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// OCP e4m3fn byte -> float (bias 7, subnormals m * 2^-9; 0x7f/0xff NaN are
-// never produced by the cache writer, which saturates at 448).
-__device__ __forceinline__ float e4m3_to_f32(uint32_t v) {
-  const uint32_t e = (v >> 3) & 0xfu, m = v & 7u;
-  float f = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * 0.001953125f;
-  return (v & 0x80u) ? -f : f;
+// Four OCP e4m3fn bytes (one dword, byte 0 first) dequantised with `scale`
+// and rounded to bf16 pairs: lo = bytes 0-1, hi = bytes 2-3. gfx950's
+// v_cvt_pk_f32_fp8 decodes OCP e4m3fn (bias 7, subnormals m * 2^-9) exactly,
+// two bytes per instruction; 0x7f / 0xff (NaN) are never written by the
+// cache writer, which saturates at 448.
+__device__ __forceinline__ void e4m3x4_to_bf16(uint32_t w, float scale, uint32_t& lo, uint32_t& hi) {
+  const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  lo = pack2<__bf16>(a[0] * scale, a[1] * scale);
+  hi = pack2<__bf16>(b[0] * scale, b[1] * scale);
 }
 
 // 16x16x32: A = 8 values of row l%16 (k = 8*(l/16)..), B likewise by column
@@ -181,19 +185,6 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 63] known only at run time
-__device__ __forceinline__ void wait_vm_rt(int n) {
-  switch (n) {
-#define SAS_WAITCASE(k) case k: wait_vm<k>(); break;
-#define SAS_WAITCASE8(k) SAS_WAITCASE(k) SAS_WAITCASE(k + 1) SAS_WAITCASE(k + 2) SAS_WAITCASE(k + 3) \
-    SAS_WAITCASE(k + 4) SAS_WAITCASE(k + 5) SAS_WAITCASE(k + 6) SAS_WAITCASE(k + 7)
-    SAS_WAITCASE8(0) SAS_WAITCASE8(8) SAS_WAITCASE8(16) SAS_WAITCASE8(24)
-    SAS_WAITCASE8(32) SAS_WAITCASE8(40) SAS_WAITCASE8(48) SAS_WAITCASE8(56)
-#undef SAS_WAITCASE8
-#undef SAS_WAITCASE
-    default: wait_vm<0>(); break;
-  }
 }
 __device__ __forceinline__ void wait_lgkm0() {
   __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
@@ -351,8 +342,11 @@ __device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int
       if (r < nr && p.scenario == SAS_SCFA && j < s1 && j >= wincap)
         idxv[r] = p.cmp_idx[(size_t)t * p.K + (j - wincap)];
     }
+    // act_q == NULL: q_prefix is cu_seqlens_q [B + 1] and a query length is
+    // the difference of two entries (loaded in the same round trip)
+    const bool cu = p.act_q == nullptr;
     int qp0 = INT_MAX, aq0 = 0, akv0 = 0;
-    if (lane < p.B) { qp0 = p.q_prefix[lane]; aq0 = p.act_q[lane]; akv0 = p.act_kv[lane]; }
+    if (lane < p.B) { qp0 = p.q_prefix[lane]; aq0 = cu ? p.q_prefix[lane + 1] : p.act_q[lane]; akv0 = p.act_kv[lane]; }
     // token -> (batch, position): largest b with q_prefix[b] <= t (q_prefix is
     // non-decreasing), one ballot per 64 batches
     int b = 0, aq = 0, akv = 0, qpb = 0;
@@ -363,12 +357,13 @@ __device__ __forceinline__ void resolve(const FwdParams& p, Tok& k, int tid, int
       for (int c = 64; n == 64 && c < p.B; c += 64) {
         const int i = c + lane;
         int qpi = INT_MAX, aqi = 0, akvi = 0;
-        if (i < p.B) { qpi = p.q_prefix[i]; aqi = p.act_q[i]; akvi = p.act_kv[i]; }
+        if (i < p.B) { qpi = p.q_prefix[i]; aqi = cu ? p.q_prefix[i + 1] : p.act_q[i]; akvi = p.act_kv[i]; }
         m = __ballot(qpi <= t);
         n = __popcll(m);
         if (n) { b = c + n - 1; qpb = __shfl(qpi, n - 1); aq = __shfl(aqi, n - 1); akv = __shfl(akvi, n - 1); }
       }
     }
+    if (cu) aq -= qpb;   // end of the batch's tokens -> its query length
     const int spos = t - qpb;
     const bool padded = spos < 0 || spos >= aq;
     const int sg = akv - aq + spos;                              // causal position

@@ -83,8 +83,11 @@ int sas_metadata_v1(const SasMetaParams* p, int32_t* out /* [SAS_META_SIZE] */);
  * (sparse_attn_sharedkv_tilelang/kernel.py:158-178) plus dims and strides.
  * q/out are flat token-major [T, H, D] / [T, H, DV]; q_prefix/act_q give each
  * batch's first packed token and query length (TND: cu_seqlens_q[:-1] and
- * lengths; BSND: b*S_max and S_max). Caches are [num_blocks, block_size, 1,
- * row] with row = D elements (bf16/fp16) or 656 bytes (fp8 rows).
+ * lengths; BSND: b*S_max and S_max). With act_q = NULL, q_prefix is
+ * cu_seqlens_q itself ([B + 1], the lengths being its differences), so a
+ * TND caller passes its device cu_seqlens_q unchanged. Caches are
+ * [num_blocks, block_size, 1, row] with row = D elements (bf16/fp16) or 656
+ * bytes (fp8 rows).
  */
 typedef struct SasFwdArgs {
   const void* q;                 /* [T, H, D] q_dtype */
@@ -93,8 +96,8 @@ typedef struct SasFwdArgs {
   const void* cmp_kv;            /* paged compressed KV (CFA/SCFA) or NULL */
   const int32_t* cmp_block_table;/* [B, cmp_bt_stride] or NULL */
   const int32_t* cmp_indices;    /* [T, 1, K] (SCFA) or NULL */
-  const int32_t* q_prefix;       /* [B] */
-  const int32_t* act_q;          /* [B] */
+  const int32_t* q_prefix;       /* [B], or [B + 1] = cu_seqlens_q when act_q is NULL */
+  const int32_t* act_q;          /* [B] or NULL */
   const int32_t* act_kv;         /* [B] seqused_kv */
   const float* sinks;            /* [H] */
   void* out;                     /* [T, H, DV] q_dtype */

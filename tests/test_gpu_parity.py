@@ -491,3 +491,78 @@ def test_prepared_call_replays_in_a_hip_graph():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(call.out, ref_out) and torch.equal(call.lse, ref_lse), f"replay {i}"
+
+
+def test_api_repeated_calls_read_current_values():
+    """The drop-in call caches its argument resolution per signature
+    (shapes, dtypes, device addresses, scalars, stream): repeated calls must
+    still read the current values of every input. Host sequence lengths
+    changed in place, device q / indices rewritten in place, and a fresh q
+    tensor each give the oracle's result for the values at that call."""
+    inp = _small(B=3, H=64, q_lens=[1, 2, 1], kv_lens=[900, 700, 300], K=64, seed=5)
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    kw.update(cu_seqlens_q=inp.cu_seqlens_q.clone(), seqused_kv=inp.seqused_kv.clone())   # host
+    from dataclasses import replace
+
+    def check(cur, name):
+        out, lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+        torch.cuda.synchronize()
+        ref_out, ref_lse = _oracle(cur)
+        _check_baseline(out.cpu(), lse.cpu(), ref_out, ref_lse, name)
+
+    check(inp, "first call")
+    check(inp, "cached call")
+    kw["seqused_kv"][:] = torch.tensor([850, 650, 290], dtype=torch.int32)   # host lengths, same tensor
+    check(replace(inp, seqused_kv=kw["seqused_kv"].clone(), kv_lens=[850, 650, 290]), "host lengths changed")
+    g = torch.Generator().manual_seed(9)
+    newq = torch.randn(inp.q.shape, generator=g).to(inp.q.dtype)
+    d.q.copy_(newq.cuda())                                                   # device q, same address
+    cur = replace(inp, q=newq, seqused_kv=kw["seqused_kv"].clone(), kv_lens=[850, 650, 290])
+    check(cur, "q rewritten in place")
+    d = replace(d, q=newq.cuda().clone())                                    # a fresh q tensor
+    check(cur, "fresh q tensor")
+
+
+def _fp8_code_rows(T, seed=0):
+    """T 656-byte fp8 rows whose latent bytes run through every non-NaN
+    e4m3fn code (0x00-0x7e, 0x80-0xfe) at several per-group scales."""
+    codes = torch.tensor([c for c in range(256) if c not in (0x7F, 0xFF)], dtype=torch.uint8)
+    g = torch.Generator().manual_seed(seed)
+    rows = torch.zeros(T, 656, dtype=torch.uint8)
+    lat = codes.repeat((T * 512 + codes.numel() - 1) // codes.numel())[:T * 512]
+    rows[:, :512] = lat[torch.randperm(T * 512, generator=g)].reshape(T, 512)
+    scales = torch.tensor([1.0, 0.0371, 3.5e-3, 117.25], dtype=torch.float32)
+    sc = scales[torch.randint(0, 4, (T, 4), generator=g)]
+    rows[:, 512:528] = sc.contiguous().view(torch.uint8).reshape(T, 16)
+    rows[:, 528:] = torch.randn(T, 64, generator=g).to(torch.bfloat16).view(torch.uint8).reshape(T, 128)
+    return rows
+
+
+@pytest.mark.parametrize("H,scenario", [(64, 1), (16, 3), (64, 3)], ids=["exact_h64", "dec_h16", "stream_h64"])
+def test_fp8_dequant_bit_exact_through_one_row_windows(H, scenario):
+    """Each token attends to exactly one cache row (window of one row, no
+    compressed rows, a sink at -3e4): P = 1, l = 1, so the output is that
+    row's V channels as the kernel dequantised them, bf16(e4m3 x scale),
+    compared bit for bit with the codec over every non-NaN code. Covers the
+    exact-window schedule (window-only call), the register-streamed decode
+    kernel (16 heads) and the streaming kernel (64 heads)."""
+    T, bs = 96, 16
+    rows = _fp8_code_rows(T)
+    cache = rows.reshape(T // bs, bs, 1, 656)
+    bt = torch.arange(T // bs, dtype=torch.int32).reshape(1, -1)
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(T, H, 576, generator=g).to(torch.bfloat16)
+    kw = dict(ori_kv=cache.cuda(), ori_block_table=bt.cuda(), cu_seqlens_q=torch.tensor([0, T], dtype=torch.int32),
+              seqused_kv=torch.tensor([T], dtype=torch.int32), sinks=torch.full((H,), -3.0e4),
+              softmax_scale=1 / 24.0, ori_win_left=0)
+    if scenario == 3:
+        kw.update(cmp_kv=cache.cuda(), cmp_block_table=bt.cuda(), cmp_ratio=4,
+                  cmp_sparse_indices=torch.full((T, 1, 16), -1, dtype=torch.int32).cuda())
+    out = sparse_attn_sharedkv(q.cuda(), **kw)
+    torch.cuda.synchronize()
+    want = paged.dequantize_kv_fp8(rows)[:, :512].to(torch.bfloat16)      # row t is token t's only key
+    got = out.cpu()
+    for h in range(H):   # by value: code 0x80 (-0.0) accumulates to +0.0
+        assert torch.equal(got[:, h].float(), want.float()), \
+            f"head {h}: {int((got[:, h].float() != want.float()).sum())} channels differ"
