@@ -305,10 +305,10 @@ struct Fwd {
       if ((ks & 1) && ks / 2 < C::OPS) dma(ks / 2);
       if constexpr (kMid) mid(ks);
     }
-#pragma unroll
-    for (int o = C::KSQ / 2; o < C::OPS; ++o) dma(o);
     // schedule: the prefetch reads first, then per k-step MT MFMAs + RT reads
-    // (+ a share of the other step's VALU work)
+    // (+ a share of the other step's VALU work). Placed before the remaining
+    // DMA issues: a wave-dependent guard there starts a new basic block, and
+    // these groups order only the instructions of their own block.
     __builtin_amdgcn_sched_group_barrier(0x100, RT * kPfK, 0);
 #pragma unroll
     for (int ks = 0; ks < C::KSQ; ++ks) {
@@ -316,6 +316,8 @@ struct Fwd {
       if (ks + kPfK < C::KSQ) __builtin_amdgcn_sched_group_barrier(0x100, RT, 0);
       if constexpr (kMid) __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
     }
+#pragma unroll
+    for (int o = C::KSQ / 2; o < C::OPS; ++o) dma(o);
   }
 
   // smax: mask, scale and sink-seeded online softmax of a finished S^T; P
@@ -679,9 +681,90 @@ struct Fwd {
     }
   }
 
+  // -- software-pipelined loop of the 8-wave channel-split kernel -----------
+  // (64-head workgroups, one key-group: the prefill configuration.) The two
+  // waves of a 16-head pair each sum S over half of D and exchange their
+  // halves through LDS. Iteration it, after one workgroup barrier, reads the
+  // exchanged S of step it, then runs the QK^T MFMAs of step it + 1 with the
+  // softmax of step it interleaved between them (independent work: the
+  // matrix pipe and the VALU overlap), writes its S half of step it + 1 to
+  // the other exchange buffer, and runs P.V of step it. Steps it + 1 and it
+  // use two ring slots; the third, freed by P.V of step it - 1 before the
+  // barrier, receives the DMA of step it + 2. One barrier per step instead of
+  // two (step + exchange).
+  static constexpr bool kPipe8 = !KVF && C::Q2 && C::KW == 1 && C::NST == 3 && NW == 8;
+  __device__ __forceinline__ f32x4* xs_buf(int b) const {
+    return reinterpret_cast<f32x4*>(lds_ring + C::kRingRows * kChunksMax) + b * (NW * C::MT * 64);
+  }
+  // Q2 piece (head tile ht, row tile rt, channel half c)
+  __device__ __forceinline__ int piece(int ht, int rt, int c) const { return ((ht * 2 + rt) * 2 + c) * 64 + lane; }
+  __device__ __forceinline__ void xs_write(int b, const f32x4 (&sacc)[C::MT]) const {
+    f32x4* xs = xs_buf(b);
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt) xs[piece((hw & ~1) + mt, hw & 1, cs)] = sacc[mt];
+  }
+  __device__ __forceinline__ void xs_read(int b, f32x4 (&sacc)[C::MT]) const {
+    const f32x4* xs = xs_buf(b);
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt) sacc[mt] = xs[piece(hw, mt, 0)] + xs[piece(hw, mt, 1)];
+  }
+  template <int J>
+  __device__ __forceinline__ void pipe8_j(int it0) {
+    const int it = it0 + J;
+    if (it >= nsteps) return;   // uniform: one key-group
+    constexpr int Jn = (J + 1) % 3, Jf = (J + 2) % 3;
+    const bool nxt = it + 1 < nsteps;
+    // my DMA of step it + 1 (the only one in flight) has landed; after the
+    // barrier every wave's has, every S half of step it is written, and
+    // every wave has finished P.V of step it - 1 (slot Jf is free)
+    wait_vm<0>();
+    lds_barrier();
+    f32x4 sc[C::MT], dummy[C::MT];
+    xs_read(it & 1, sc);
+    float sv[C::MT][4], lsum = 0.f;
+    uint32_t pk[2 * C::MT];
+    smax_a<false>(sc, dummy, it, sv);
+    const bool more = it + 2 < nsteps;
+    Dma d;
+    if (more) prep(d, Jf, it + 2);
+    if (nxt) {
+      f32x4 sn[C::MT], so[C::MT];
+      qk<true>(slot(Jn), sn, so, [&](int o) { if (more) fire(d, o); }, [&](int ks) {
+        if (ks < kSmaxB) smax_b(ks, sv, lsum, pk);
+      });
+#pragma unroll
+      for (int e = C::KSQ; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
+      xs_write((it + 1) & 1, sn);
+    } else {
+#pragma unroll
+      for (int e = 0; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
+    }
+    pv(slot(J), pk, [](int) {});
+  }
+
+  __device__ __forceinline__ void run_pipe8() {
+    if (nsteps <= 0) return;   // uniform over the workgroup
+    issue(0, 0);
+    if (nsteps > 1) issue(1, 1);
+    wait_steps(nsteps > 1 ? 1 : 0);   // my part of step 0
+    lds_barrier();
+    f32x4 s0[C::MT], so[C::MT];
+    qk(slot(0), s0, so, [](int) {});
+    xs_write(0, s0);
+    for (int it0 = 0; it0 < nsteps; it0 += 3) {
+      pipe8_j<0>(it0);
+      pipe8_j<1>(it0);
+      pipe8_j<2>(it0);
+    }
+  }
+
   __device__ __forceinline__ void run() {
     if constexpr (kPipe) {
       run_pipe();
+      return;
+    }
+    if constexpr (kPipe8) {
+      run_pipe8();
       return;
     }
     if constexpr (!KVF) {
@@ -888,11 +971,15 @@ sas_fwd_kernel(const FwdParams p) {
   // Q^T operand in registers (head hq, channels ks*32 + 8g .. +8): with QL
   // through LDS (DMA by the waves that do no slot resolution, at once), else
   // loaded behind the block-table reads of the slot resolution
+  // QL: the query rows depend on the token index only, so waves 4-7 (which
+  // do no slot resolution) issue their DMA before anything else, under the
+  // latency of the index round trip, and are done issuing by the time the
+  // compaction barrier waits for them
+  if constexpr (C::QL) {
+    if (wave >= 4) f.q_dma(k, wave);
+  }
   resolve<256, C::ROWB>(p, k, tid, lane, wave, [&] {
-    if constexpr (C::QL) {
-      if (wave >= 4) f.q_dma(k, wave);
-      return;
-    }
+    if constexpr (C::QL) return;
     const uint4* qp = reinterpret_cast<const uint4*>(p.q + ((size_t)k.t * p.H + hq) * D * 2);
 #pragma unroll
     for (int n = 0; n < C::NQ; ++n) {
