@@ -372,7 +372,7 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   if (ns <= 0) {
     // enough (token, head groups, split) workgroups for 8 waves per CU
     const long long items = a->T * fp.nhg;
-    const long long want = (2 * kCus / ng + items - 1) / items;
+    const long long want = (2 * device_cus() / ng + items - 1) / items;
     ns = (int)std::min<long long>(want, (nslots + 63) / 64);
   }
   ns = std::max(1, std::min(ns, 64));

@@ -1291,22 +1291,36 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   // maximum (golden's one window tile). An explicit split count above 1 or
   // 8 waves selects the streaming schedule instead.
   pl->exact = a->scenario == SAS_SWA && pl->nslots <= kLdsRows && ns <= 1 && (a->waves == 0 || a->waves == 4);
+  const bool fp8 = a->kv_dtype == SAS_DT_FP8_E4M3_ROW656;
+  // Every workgroup of a token runs on the token's XCD (item_index deals
+  // tokens round-robin over the XCDs, blockIdx % 8): with one workgroup per
+  // CU, a grid fills the chip in one round when each XCD's share,
+  // ceil(T / 8) tokens x head groups x splits, fits its CUs. A second round
+  // roughly doubles a decode call (31-token, 128-head decode with 5 splits
+  // of 64 heads: 43.8 µs, 4 splits: 28.7 µs).
+  const int cus = sas::device_cus();
+  const long long cus_x = std::max(1, cus / kXcds);
+  const long long tpx = (T + kXcds - 1) / kXcds;
+  auto one_round_splits = [&](int h) { return std::max<long long>(1, cus_x / (tpx * (a->H / (16 * h)))); };
   if (hw <= 0) {
-    // Heads sharing one gathered tile inside a workgroup (16 per wave). With
-    // many tokens every workgroup holds 64 heads: each row crosses L2 -> CU
-    // once per token. With few tokens, 32-head groups (2 head-waves x 2
-    // key-groups) spread a token over twice the workgroups for the same split
-    // count: half the fp32 split partials of 64-head groups at the same grid
-    // size, for each row read twice through L2 (measured best for the
-    // 32-token, 64-head decode).
-    if (a->H % 64 == 0 && T * (a->H / 64) >= 2 * kCus) hw = 4;
+    // Heads sharing one gathered tile inside a workgroup (16 per wave); each
+    // row crosses L2 -> CU once per head group. With many tokens every
+    // workgroup holds 64 heads. With few, 32-head groups (2 head-waves x 2
+    // key-groups, 8 waves) while they still allow 4 splits in one round:
+    // half the rows per split at equal grid size, and fewer partials to
+    // merge (32-token, 64-head decode: 18.4 µs at 32 heads x 4 splits,
+    // 21.1 µs at 64 heads x 8 splits); else 64-head groups, which leave room
+    // for twice the splits (31-token, 128-head decode: 28.7 µs at 64 x 4
+    // against 32.4 µs at 32 x 2). fp8 rows take 64-head groups (4 waves
+    // only; 8-token, 128-head fp8 decode: 25.6 µs against 31.7 µs).
+    if (a->H % 64 == 0 && T * (a->H / 64) >= 2 * cus) hw = 4;
+    else if (a->H % 64 == 0 && (fp8 || one_round_splits(2) < 4)) hw = 4;
     else if (a->H % 32 == 0) hw = 2;
     else hw = 1;
   }
   if (hw != 1 && hw != 2 && hw != 4) return sas::set_error(SAS_EINVAL, "head_waves must be 1, 2 or 4");
   while (hw > 1 && a->H % (16 * hw)) hw >>= 1;
   int nw = a->waves;
-  const bool fp8 = a->kv_dtype == SAS_DT_FP8_E4M3_ROW656;
   // 8 waves: two per SIMD, a pair per 16 heads splitting both the QK^T and
   // the O channels; the second wave on a SIMD overlaps the other's LDS and
   // softmax latencies (measured: 4K prefill 593 vs 650 µs, 32-token decode
@@ -1320,13 +1334,12 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   pl->nhg = (int)a->H / (16 * hw);
   if (pl->exact) ns = 1;
   if (ns <= 0) {
-    // one workgroup per CU: split the slots until the grid covers the chip,
-    // keeping every split long enough for one step of each key-group
-    const long long items = T * pl->nhg;
-    const long long want = (kCus + items - 1) / items;
-    const int min_sps = hw == 1 ? 64 : hw == 2 ? 64 : 32;
-    const int max_by_step = std::max(1, (pl->nslots + min_sps - 1) / min_sps);
-    ns = (int)std::min<long long>(std::max<long long>(want, 1), max_by_step);
+    // as many splits as fill each XCD's CUs in one round, each split at
+    // least min_sps slots (1-token, 16-head decode: 15.5 µs at 4 splits of
+    // 48 slots, 16.1 µs at 3 of 64)
+    const int min_sps = hw == 1 ? 48 : 64;
+    const int max_by_len = std::max(1, (pl->nslots + min_sps - 1) / min_sps);
+    ns = (int)std::min<long long>(one_round_splits(hw), max_by_len);
   }
   ns = std::max(1, std::min(ns, kMaxCombineSplits));
   int sps = (pl->nslots + ns - 1) / ns;
@@ -1478,7 +1491,7 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   // the kernel instead of leaving the L2 dirty for the writeback at its end
   // (C2 decode: 22.7 -> 22.0 µs); with a second wave of workgroups, or small
   // partials, the L2 copy the combine reads is worth more (C4, C1 slower).
-  fp.part_nt = pl.nsplit > 1 && nblocks <= kCus && pl.ws >= (size_t(4) << 20);
+  fp.part_nt = pl.nsplit > 1 && nblocks <= sas::device_cus() && pl.ws >= (size_t(4) << 20);
   // An output far beyond the L2s (4K prefill: 268 MB) streams out instead of
   // evicting the cache rows the next tokens gather (C3: 586 -> 571 µs).
   fp.out_nt = pl.nsplit == 1 && (size_t)a->T * a->H * kDV * 2 >= (size_t(16) << 20);

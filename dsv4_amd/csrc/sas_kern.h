@@ -14,6 +14,8 @@
 #include "../../include/sas.h"
 #include "sas_common.h"
 
+#include <atomic>
+
 #define LDS_AS __attribute__((address_space(3)))
 
 namespace sas {
@@ -23,13 +25,33 @@ constexpr int kMaxSlots = 1280;   // slot range one workgroup may own
 constexpr int kRoundsMax = kMaxSlots / 256;  // slot rounds at 256 threads
 constexpr int kMaxWaves = 8;
 constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dealt round-robin
-constexpr int kCus = 256;         // MI355X compute units (one forward workgroup each)
 constexpr int kRow656 = 656;      // fp8 cache row bytes
 constexpr int kChunksMax = 72;    // 16-byte chunks of a 576-channel bf16 row
 constexpr int kLdsRows = 128;     // rows of ring storage per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazyLog2 = 8.f;   // O / l rescale threshold (log2 units)
+
+// Compute units of the current device (one forward workgroup each): the
+// grid planners fill them. Queried once per device; 256 (MI355X) when no
+// device answers, e.g. a plan query on a host without a GPU.
+inline int device_cus() {
+  constexpr int kMaxDev = 64, kDefault = 256;
+  static std::atomic<int> cached[kMaxDev] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+    (void)hipGetLastError();
+    return kDefault;
+  }
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return kDefault;
+  }
+  cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -25,6 +25,13 @@ def test_header_declares_the_exported_set():
     assert _declared() == sorted(_lib.EXPORTED)
 
 
+def test_python_constants_match_the_header():
+    text = open(HEADER).read()
+    for name in ("SAS_FWD_NO_COMBINE", "SAS_META_SIZE"):
+        m = re.search(r"^#define\s+%s\s+(\d+)" % name, text, flags=re.M)
+        assert m and int(m.group(1)) == getattr(_lib, name), name
+
+
 @pytest.mark.parametrize("sym", _declared())
 def test_symbol_exported(sym):
     assert hasattr(_lib.lib(), sym), f"libsas.so does not export {sym}"
