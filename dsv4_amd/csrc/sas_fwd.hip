@@ -667,9 +667,10 @@ struct Fwd {
       __syncthreads();   // read before the epilogue reuses lds_ml
     }
     // every key-group rounds against M = max(sink, all rows); the sink's
-    // (1 at its own maximum) term is counted once, by key-group 0
+    // (1 at its own maximum) term is counted once, by key-group 0. A split
+    // of several (sink_log2 = -inf) leaves the sink to the merge.
     m_run = fmaxf(mloc, sink_log2);
-    l_run = kw == 0 ? __builtin_amdgcn_exp2f(sink_log2 - m_run) : 0.f;
+    l_run = kw == 0 && sink_log2 > -INFINITY ? __builtin_amdgcn_exp2f(sink_log2 - m_run) : 0.f;
 #pragma unroll
     for (int j = 0; j < C::NST; ++j) {
       if (j >= nsteps) break;
@@ -1015,7 +1016,7 @@ sas_fwd_kernel(const FwdParams p) {
 #pragma unroll
   for (int i = 0; i < C::NTL; ++i) f.acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if constexpr (EXW) f.run_exact(wave, sink * kLog2e);
+  if constexpr (EXW) f.run_exact(wave, p.nsplit == 1 ? sink * kLog2e : -INFINITY);
   else f.run();
   epilogue<HW, NW, C::CS, QT>(p, k, tid, wave, lane, f.m_run, f.l_run, f.acc);
 }
@@ -1289,7 +1290,8 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   // Window-only calls whose window fits the ring run the exact-window
   // schedule: one split, 4 waves, P rounded against the window's final
   // maximum (golden's one window tile). An explicit split count above 1 or
-  // 8 waves selects the streaming schedule instead.
+  // 8 waves selects the streaming schedule instead. (16-head groups may take
+  // the exact schedule with splits too, below.)
   pl->exact = a->scenario == SAS_SWA && pl->nslots <= kLdsRows && ns <= 1 && (a->waves == 0 || a->waves == 4);
   const bool fp8 = a->kv_dtype == SAS_DT_FP8_E4M3_ROW656;
   // Every workgroup of a token runs on the token's XCD (item_index deals
@@ -1342,6 +1344,15 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
     ns = (int)std::min<long long>(one_round_splits(hw), max_by_len);
   }
   ns = std::max(1, std::min(ns, kMaxCombineSplits));
+  // 16-head groups run the exact schedule when a split's rows fit the ring
+  // (every row gathered at once, no per-step barriers; 1-token, 16-head
+  // decode: 12.7 µs against 15.5 µs for the register-streaming decode
+  // kernel), taking the splits that make them fit if one round holds them
+  if (!pl->exact && hw == 1 && (a->waves == 0 || a->waves == 4)) {
+    const int fit = (pl->nslots + kLdsRows - 1) / kLdsRows;
+    if (a->num_splits <= 0 && ns < fit && fit <= std::min<long long>(one_round_splits(1), kMaxCombineSplits)) ns = fit;
+    pl->exact = (pl->nslots + ns - 1) / ns <= kLdsRows;
+  }
   int sps = (pl->nslots + ns - 1) / ns;
   if (sps > kMaxSlots) {
     ns = (pl->nslots + kMaxSlots - 1) / kMaxSlots;

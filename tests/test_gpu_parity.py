@@ -396,6 +396,20 @@ def test_swa_exact_and_streaming_schedules_agree():
     assert e_ex <= e_st
 
 
+@pytest.mark.parametrize("scenario,K", [(3, 64), (2, 0), (3, 400)], ids=["scfa_k64", "cfa", "scfa_k400"])
+def test_h16_exact_and_register_streamed_kernels_agree(scenario, K):
+    """16-head groups: the exact schedule (the default while a split's rows
+    fit the 128-row ring, with or without splits) and the register-streamed
+    decode kernel (selected by waves=8) both meet the tolerance against
+    golden, with 1, 2 and the planned number of splits."""
+    inp = _small(B=3, H=16, q_lens=[1, 2, 1], kv_lens=[3000, 700, 129], K=K, scenario=scenario, seed=11)
+    ref_out, ref_lse = _oracle(inp)
+    for ns in (0, 1, 2):
+        for waves in (0, 8):
+            out, lse, got_ns = _run(inp, num_splits=ns, waves=waves)
+            _check_baseline(out, lse, ref_out, ref_lse, f"h16 splits={ns}->{got_ns} waves={waves}")
+
+
 def test_bsnd_layout_with_padding():
     """BSND q [B, S, N, D] with per-batch lengths from cu_seqlens_q: padded
     slots come back as zeros (golden.py:97), valid ones match TND."""
@@ -539,14 +553,15 @@ def _fp8_code_rows(T, seed=0):
     return rows
 
 
-@pytest.mark.parametrize("H,scenario", [(64, 1), (16, 3), (64, 3)], ids=["exact_h64", "dec_h16", "stream_h64"])
-def test_fp8_dequant_bit_exact_through_one_row_windows(H, scenario):
+@pytest.mark.parametrize("H,scenario,waves", [(64, 1, 0), (16, 3, 0), (16, 3, 8), (64, 3, 0)],
+                         ids=["exact_h64", "exact_h16", "dec_h16", "stream_h64"])
+def test_fp8_dequant_bit_exact_through_one_row_windows(H, scenario, waves):
     """Each token attends to exactly one cache row (window of one row, no
     compressed rows, a sink at -3e4): P = 1, l = 1, so the output is that
     row's V channels as the kernel dequantised them, bf16(e4m3 x scale),
     compared bit for bit with the codec over every non-NaN code. Covers the
-    exact-window schedule (window-only call), the register-streamed decode
-    kernel (16 heads) and the streaming kernel (64 heads)."""
+    exact schedule (64 and 16 heads), the register-streamed decode kernel
+    (16 heads, selected by waves=8) and the streaming kernel (64 heads)."""
     T, bs = 96, 16
     rows = _fp8_code_rows(T)
     cache = rows.reshape(T // bs, bs, 1, 656)
@@ -559,8 +574,10 @@ def test_fp8_dequant_bit_exact_through_one_row_windows(H, scenario):
     if scenario == 3:
         kw.update(cmp_kv=cache.cuda(), cmp_block_table=bt.cuda(), cmp_ratio=4,
                   cmp_sparse_indices=torch.full((T, 1, 16), -1, dtype=torch.int32).cuda())
-    out = sparse_attn_sharedkv(q.cuda(), **kw)
+    call = prepare_sparse_attn_sharedkv(q.cuda(), waves=waves, **kw)
+    call.launch()
     torch.cuda.synchronize()
+    out = call.out
     want = paged.dequantize_kv_fp8(rows)[:, :512].to(torch.bfloat16)      # row t is token t's only key
     got = out.cpu()
     for h in range(H):   # by value: code 0x80 (-0.0) accumulates to +0.0
