@@ -122,10 +122,22 @@ def measured_peaks():
     ms, _ = time_launches(lambda i, st: torch.matmul(a, b, out=c), 1, 20, 3)
     gemm_tf = 2 * m ** 3 / (ms / 20 * 1e-3) / 1e12
     del a, b, c
+    # fp32 atomic adds (the backward's row gradients): index_add_ of 2^17
+    # random 576-float rows into 6144 rows (the C3 cache's row count)
+    rows, n = 6144, 1 << 17
+    g = torch.Generator(device="cuda").manual_seed(5)
+    dst = torch.zeros(rows, 576, device="cuda")
+    src = torch.randn(n, 576, device="cuda", generator=g)
+    idx = torch.randint(0, rows, (n,), device="cuda", generator=g)
+    ms, _ = time_launches(lambda i, st: dst.index_add_(0, idx, src), 1, 10, 2)
+    atom_g = n * 576 / (ms / 10 * 1e-3) / 1e9
+    del dst, src, idx
     torch.cuda.synchronize()
     return dict(hbm_spec_gbs=HBM_PEAK_GBS, hbm_copy_measured_gbs=round(copy_gbs, 1),
                 bf16_spec_tflops=BF16_PEAK_TFLOPS, bf16_gemm_measured_tflops=round(gemm_tf, 1),
-                how="copy: torch copy_ of 2 GiB (read + write bytes); gemm: torch.matmul 8192^3 bf16")
+                fp32_atomic_measured_g_per_s=round(atom_g, 1),
+                how="copy: torch copy_ of 2 GiB (read + write bytes); gemm: torch.matmul 8192^3 bf16; "
+                    "atomics: torch index_add_ of 2^17 x 576 fp32 into 6144 rows")
 
 
 def usable_cores():
@@ -361,11 +373,16 @@ def bench_decode_configs(names, steps, flush):
 BWD_FLOP_PER_PAIR_HEAD = 2 * (3 * 576 + 2 * 512)   # q.k, dO.v, dq, dk (D = 576), dv (512)
 
 
-def bench_backward(dec_inp, pre_inp):
+def bench_backward(dec_inp, pre_inp, atomic_peak=None):
     """sas_bwd_v1 on the C2 decode and C3 prefill inputs: the forward's out /
     LSE, a random bf16 dO, gradient buffers allocated once (the kernel's own
     time: the cache gradients accumulate across the timed launches). Useful
-    FLOP per (token, key, head): 2 x (3 x 576 + 2 x 512) = 5504."""
+    FLOP per (token, key, head): 2 x (3 x 576 + 2 x 512) = 5504. Row-gradient
+    atomics per launch: one fp32 add per (token, key, head group of
+    heads_per_workgroup, channel), counted here (with several KV splits the
+    dq shares add atomically too, not counted). The launch's atomic rate
+    against the measured fp32 atomic peak is the bound that applies (the FLOP
+    rate is far below the MFMA peak)."""
     from dsv4_amd import cases
     from dsv4_amd.api import prepare_sparse_attn_sharedkv_backward, sparse_attn_sharedkv
     res = {"kernel": "sas_bwd_kernel (MFMA scores, dq and dkv; fp32 atomics for dkv)",
@@ -383,8 +400,14 @@ def bench_backward(dec_inp, pre_inp):
         pairs = cases.gathered_rows(inp)
         flop = pairs * inp.cfg.H * BWD_FLOP_PER_PAIR_HEAD
         tfl = flop / (us * 1e-6) / 1e12
+        hpw = 32 if inp.cfg.H % 32 == 0 else 16
+        D = inp.q.shape[-1]
+        atomics = pairs * (inp.cfg.H // hpw) * D
+        rate = atomics / (us * 1e-6) / 1e9
         res[key] = dict(workload=inp.cfg.name, us_per_call=round(us, 1), useful_flop=flop,
-                        tflops=round(tfl, 2), mfma_frac=round(tfl / BF16_PEAK_TFLOPS, 5))
+                        tflops=round(tfl, 2), mfma_frac=round(tfl / BF16_PEAK_TFLOPS, 5),
+                        heads_per_workgroup=hpw, fp32_row_atomics=atomics, atomic_g_per_s=round(rate, 1),
+                        atomic_frac=round(rate / atomic_peak, 3) if atomic_peak else None)
         del pb, out, lse, dout
     return res
 
@@ -528,16 +551,18 @@ def main():
     if not args.no_peaks:
         peaks = measured_peaks()
         log(f"peaks: copy {peaks['hbm_copy_measured_gbs']} GB/s, "
-            f"bf16 GEMM {peaks['bf16_gemm_measured_tflops']} TFLOP/s")
+            f"bf16 GEMM {peaks['bf16_gemm_measured_tflops']} TFLOP/s, "
+            f"fp32 atomics {peaks['fp32_atomic_measured_g_per_s']} G/s")
 
     # ---------------- backward (C2 decode, C3 prefill) ----------------------
     backward = None
     if not args.no_backward:
-        backward = bench_backward(inp, pinp if prefill is not None else None)
+        backward = bench_backward(inp, pinp if prefill is not None else None,
+                                  peaks["fp32_atomic_measured_g_per_s"] if peaks else None)
         for k_ in ("decode", "prefill"):
             if backward.get(k_):
                 log(f"backward {k_}: {backward[k_]['us_per_call']:.1f} us/call, "
-                    f"{backward[k_]['tflops']:.1f} TFLOP/s")
+                    f"{backward[k_]['tflops']:.1f} TFLOP/s, {backward[k_]['atomic_g_per_s']:.1f} G atomics/s")
 
     # ---------------- paged-KV cache writer (fp8 rows) ------------------------
     cwrite = None
