@@ -1338,8 +1338,10 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   if (ns <= 0) {
     // as many splits as fill each XCD's CUs in one round, each split at
     // least min_sps slots (1-token, 16-head decode: 15.5 µs at 4 splits of
-    // 48 slots, 16.1 µs at 3 of 64)
-    const int min_sps = hw == 1 ? 48 : 64;
+    // 48 slots, 16.1 µs at 3 of 64; fp8 rows, which cost the 4-wave kernel
+    // more per row to stage: 8-token, 128-head decode 25.6 µs at 12 splits of
+    // 96 slots, 26.3 µs at 16 of 72)
+    const int min_sps = fp8 ? 96 : hw == 1 ? 48 : 64;
     const int max_by_len = std::max(1, (pl->nslots + min_sps - 1) / min_sps);
     ns = (int)std::min<long long>(one_round_splits(hw), max_by_len);
   }
