@@ -66,6 +66,23 @@ def test_plan_valid():
     assert ws == (0 if ns == 1 else 4 * ns * 64 * (512 * 2 + 4 * 4))   # fp16 part_o + (m, l, e, e)
 
 
+# The planner at the benchmark shapes, on the 256-CU, 8-XCD MI355X (the CU
+# count it assumes when no device answers, as here): every XCD's share of
+# workgroups, ceil(T / 8) tokens x head groups x splits, fits its 32 CUs.
+@pytest.mark.parametrize("T,H,K,fp8,want", [
+    (1, 16, 64, False, 4),       # C1: 192 slots, 16-head groups, 4 splits of 48 (exact schedule)
+    (32, 64, 512, False, 4),     # C2: 32-head groups: 4 tokens x 2 groups x 4 splits per XCD
+    (31, 128, 1024, False, 4),   # C4: 64-head groups: 4 tokens x 2 groups x 4 splits per XCD
+    (8, 128, 1024, True, 12),    # C5: fp8 rows, 64-head groups, splits of at least 96 slots
+    (4096, 64, 512, False, 1),   # C3: prefill, one split
+], ids=["C1", "C2", "C4", "C5", "C3"])
+def test_plan_at_benchmark_shapes(T, H, K, fp8, want):
+    kvd = _lib.SAS_DT_FP8_E4M3_ROW656 if fp8 else _lib.SAS_DT_BF16
+    rc, ns, ws = _plan(_valid_args(T=T, H=H, K=K, kv_dtype=kvd))
+    assert rc == _lib.SAS_OK and ns == want
+    assert ws == (0 if ns == 1 else T * ns * H * (512 * 2 + 16))
+
+
 def test_plan_explicit_splits_and_workspace():
     rc, ns, ws = _plan(_valid_args(num_splits=3))
     assert rc == _lib.SAS_OK and ns == 3
