@@ -410,6 +410,39 @@ def test_h16_exact_and_register_streamed_kernels_agree(scenario, K):
             _check_baseline(out, lse, ref_out, ref_lse, f"h16 splits={ns}->{got_ns} waves={waves}")
 
 
+def _fuzz_case(i):
+    """Seeded random configuration i: scenario, head count, window, block
+    size, compressed ratio and top-k width, head dim, dtype, fp8 rows, batch
+    of decode or short prefill rows, optional explicit split count."""
+    r = np.random.default_rng(1000 + i)
+    scenario = int(r.choice([1, 2, 3]))
+    D = int(r.choice([512, 576]))
+    dtype = torch.float16 if r.random() < 0.25 else torch.bfloat16
+    fp8 = D == 576 and dtype == torch.bfloat16 and r.random() < 0.25
+    B = int(r.integers(1, 5))
+    prefill = r.random() < 0.2
+    q_lens = [int(r.integers(8, 65)) if prefill else int(r.integers(1, 4)) for _ in range(B)]
+    kv_lens = [int(r.integers(1, 3001)) for _ in range(B)]
+    kw = dict(B=B, H=int(r.choice([16, 32, 48, 64, 128])), q_lens=q_lens, kv_lens=kv_lens,
+              K=int(r.choice([16, 100, 300, 700])) if scenario == 3 else 0,
+              ratio=int(r.choice([4, 8])), bs=int(r.choice([16, 64, 128])), D=D, scenario=scenario,
+              fp8=fp8, dtype=dtype, win=int(r.choice([0, 31, 63, 127, 255])), seed=i)
+    splits = int(r.choice([0, 0, 1, 2, 5]))
+    return kw, splits
+
+
+@pytest.mark.parametrize("i", range(64))
+def test_random_configurations_against_oracle(i):
+    """Random configurations (seeded) through the planner's own choices or an
+    explicit split count: out within atol = rtol = 2e-2, LSE within 1e-3."""
+    kw, splits = _fuzz_case(i)
+    print(f"[fuzz {i}] {kw} splits={splits}", flush=True)
+    inp = _small(**kw)
+    out, lse, ns = _run(inp, num_splits=splits)
+    ref_out, ref_lse = _oracle(inp)
+    _check_baseline(out, lse, ref_out, ref_lse, f"fuzz {i} (splits {ns})")
+
+
 def test_bsnd_layout_with_padding():
     """BSND q [B, S, N, D] with per-batch lengths from cu_seqlens_q: padded
     slots come back as zeros (golden.py:97), valid ones match TND."""
