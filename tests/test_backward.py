@@ -234,6 +234,28 @@ def test_gpu_backward_matches_oracle(name):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("i", range(24))
+def test_gpu_backward_random_configurations(i):
+    """Seeded random configurations (scenario, H, D, dtype, window, block
+    size, ratio, top-k, decode or short prefill batches), every gradient
+    element against the oracle from the GPU forward's own out / lse."""
+    from dsv4_amd.api import sparse_attn_sharedkv, sparse_attn_sharedkv_backward
+    from tests.test_gpu_parity import _fuzz_case, _small
+    kw, _ = _fuzz_case(500 + i)
+    kw["fp8"] = False   # the backward takes caches in the query dtype
+    print(f"[bwd fuzz {i}] {kw}", flush=True)
+    inp = _small(**kw)
+    d = inp.to("cuda")
+    akw = d.api_kwargs()
+    out, lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **akw)
+    g = torch.Generator().manual_seed(7 + i)
+    dout = torch.randn(out.shape, generator=g).to(inp.q.dtype)
+    dq, d_ori, d_cmp, d_sinks = sparse_attn_sharedkv_backward(dout.cuda(), d.q, out, lse, **akw)
+    torch.cuda.synchronize()
+    _check_against_oracle(f"bwd fuzz {i}", inp, dq, d_ori, d_cmp, d_sinks, _oracle_bwd(inp, dout, out, lse))
+
+
+@pytest.mark.gpu
 def test_gpu_backward_c2_decode_full():
     """The C2 workload the bench times (32 tokens, H = 64, top-k 512 +
     window 128 over 8K-32K contexts), every gradient against the oracle."""
