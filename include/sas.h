@@ -114,13 +114,18 @@ typedef struct SasFwdArgs {
   int32_t cmp_ratio;
   int32_t win_left;              /* ori_win_left (window = win_left + 1 rows) */
   float softmax_scale;
-  int32_t num_splits;            /* KV splits per token; 0 = choose automatically */
+  int32_t num_splits;            /* KV splits per token; 0 = choose automatically.
+                                    Above 1 on a window-only call, it selects the
+                                    streaming schedule over the one-split exact one */
   int32_t head_waves;            /* waves sharing each KV tile (16 heads each): 1, 2, 4;
                                     the other waves/head_waves groups stream disjoint rows;
                                     0 = choose automatically */
   int32_t flags;                 /* SAS_FWD_* bits, 0 by default */
-  int32_t waves;                 /* waves per workgroup: 4 or 8 (head_waves 1: 4);
-                                    0 = choose automatically */
+  int32_t waves;                 /* waves per workgroup: 4 or 8 (fp8 rows: 4);
+                                    0 = choose automatically. 8 also selects the
+                                    streaming schedule where a split's rows would
+                                    fit one LDS ring (window-only calls, 16-head
+                                    groups), which then runs 4 waves */
 } SasFwdArgs;
 
 /* SasFwdArgs.flags: with more than one split, stop after the split kernel and
