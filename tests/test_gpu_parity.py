@@ -396,6 +396,24 @@ def test_swa_exact_and_streaming_schedules_agree():
     assert e_ex <= e_st
 
 
+@pytest.mark.parametrize("K", [16, 300], ids=["jump_in_last_step", "jump_mid_stream"])
+def test_prefill_score_jump_moves_the_reference(K):
+    """64-head single-split prefill whose top-k rows score ~60 nats (~87 log2
+    units) above the window rows: the head max jumps far past the reference
+    the first steps set (with K = 16 in the last step, with K = 300 in a
+    middle one), so O and l are rescaled by ~2^-87 in one step. Both
+    wave layouts meet the tolerance against the fp64 oracle."""
+    inp = _small(B=1, H=64, q_lens=[300], kv_lens=[1500], K=K, seed=11)
+    inp.q[:, :, 0] = 40.0
+    inp.ori_kv[..., 0] = 0.0
+    inp.cmp_kv[..., 0] = 36.0
+    ref_out, ref_lse = _oracle(inp)
+    for waves in (0, 4):
+        out, lse, ns = _run(inp, waves=waves)
+        assert ns == 1
+        _check_baseline(out, lse, ref_out, ref_lse, f"score jump K={K} waves={waves}")
+
+
 @pytest.mark.parametrize("scenario,K", [(3, 64), (2, 0), (3, 400)], ids=["scfa_k64", "cfa", "scfa_k400"])
 def test_h16_exact_and_register_streamed_kernels_agree(scenario, K):
     """16-head groups: the exact schedule (the default while a split's rows
