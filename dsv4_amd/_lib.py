@@ -19,7 +19,7 @@ SAS_SWA, SAS_CFA, SAS_SCFA = 1, 2, 3
 SAS_META_SIZE = 1024
 SAS_FWD_NO_COMBINE = 1
 
-EXPORTED = ("sas_metadata_v1", "sas_fwd_plan", "sas_fwd_v1", "sas_fwd_noalloc_v1", "sas_combine_v1",
+EXPORTED = ("sas_metadata_v1", "sas_metadata_device_v1", "sas_fwd_plan", "sas_fwd_v1", "sas_fwd_noalloc_v1", "sas_combine_v1",
             "sas_cache_write_v1", "sas_bwd_v1", "sas_last_error", "sas_version")
 
 _i32p = C.POINTER(C.c_int32)
@@ -107,6 +107,8 @@ def lib() -> C.CDLL:
                 L = C.CDLL(LIB_PATH)
                 L.sas_metadata_v1.argtypes = [C.POINTER(SasMetaParams), _i32p]
                 L.sas_metadata_v1.restype = C.c_int
+                L.sas_metadata_device_v1.argtypes = [C.POINTER(SasMetaParams), C.c_void_p, C.c_void_p]
+                L.sas_metadata_device_v1.restype = C.c_int
                 L.sas_fwd_plan.argtypes = [C.POINTER(SasFwdArgs), _i32p, C.POINTER(C.c_size_t)]
                 L.sas_fwd_plan.restype = C.c_int
                 L.sas_fwd_v1.argtypes = [C.POINTER(SasFwdArgs), C.c_void_p]

@@ -70,6 +70,50 @@ def _int_array(t):
     return a, C.cast(a.data_ptr(), C.POINTER(C.c_int32)), a.numel()
 
 
+def _params(*, num_heads_q, num_heads_kv, head_dim, batch_size, max_seqlen_q, max_seqlen_kv, ori_topk,
+            cmp_topk, cmp_ratio, ori_mask_mode, cmp_mask_mode, ori_win_left, ori_win_right, layout_q,
+            layout_kv, has_ori_kv, has_cmp_kv, aic_core_num, aiv_core_num, keep) -> _lib.SasMetaParams:
+    """The scalar fields of SasMetaParams (the layout strings kept alive in ``keep``)."""
+    p = _lib.SasMetaParams()
+    p.num_heads_q, p.num_heads_kv, p.head_dim = int(num_heads_q), int(num_heads_kv), int(head_dim)
+    p.batch_size, p.max_seqlen_q, p.max_seqlen_kv = int(batch_size), int(max_seqlen_q), int(max_seqlen_kv)
+    p.ori_topk, p.cmp_topk, p.cmp_ratio = int(ori_topk), int(cmp_topk), int(cmp_ratio)
+    p.ori_mask_mode, p.cmp_mask_mode = int(ori_mask_mode), int(cmp_mask_mode)
+    p.ori_win_left, p.ori_win_right = int(ori_win_left), int(ori_win_right)
+    lq, lkv = str(layout_q).encode(), str(layout_kv).encode()
+    keep += [lq, lkv]
+    p.layout_q, p.layout_kv = lq, lkv
+    p.has_ori_kv, p.has_cmp_kv = int(bool(has_ori_kv)), int(bool(has_cmp_kv))
+    p.aic_core_num, p.aiv_core_num = int(aic_core_num), int(aiv_core_num)
+    return p
+
+
+def _metadata_device(dev, tensors, **scalars) -> torch.Tensor:
+    """sas_metadata_device_v1: the lengths stay on ``dev`` (int32 views or
+    copies made there), the result is a device tensor; nothing synchronises."""
+    keep = []
+    p = _params(keep=keep, **scalars)
+    names = ("cu_seqlens_q", "cu_seqlens_ori_kv", "cu_seqlens_cmp_kv", "seqused_q", "seqused_kv")
+    for name, t in zip(names, tensors):
+        n = 0
+        if t is not None and t.numel() > 0:
+            a = t.detach().reshape(-1).to(dtype=torch.int32).contiguous()
+            keep.append(a)
+            setattr(p, name, C.cast(a.data_ptr(), C.POINTER(C.c_int32)))
+            n = a.numel()
+        setattr(p, "n_" + name, n)
+    out = torch.empty(SAS_META_SIZE, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        st = torch.cuda.current_stream(dev)
+        rc = _lib.lib().sas_metadata_device_v1(C.byref(p), C.c_void_p(out.data_ptr()), C.c_void_p(st.cuda_stream))
+        _lib.check(rc, "sparse_attn_sharedkv_metadata")
+        # int32 copies made for the launch must outlive it on the stream
+        for a in keep:
+            if isinstance(a, torch.Tensor):
+                a.record_stream(st)
+    return out
+
+
 def sparse_attn_sharedkv_metadata(
     *,
     num_heads_q: int,
@@ -99,18 +143,35 @@ def sparse_attn_sharedkv_metadata(
     device: Optional[str] = None,
 ) -> torch.Tensor:
     """Return the scheduler's INT32 ``[SAS_META_SIZE]`` tensor (CPU, or on
-    ``device`` when given), as metadata.py:1018-1086 does."""
+    ``device`` when given), as metadata.py:1018-1086 does.
+
+    When ``device`` is a GPU and every sequence-length tensor given lives on
+    it, the schedule is computed there (``sas_metadata_device_v1``: one
+    kernel on the current stream, no host copy, no synchronisation), bit for
+    bit the host schedule; else on the host (``sas_metadata_v1``)."""
+    tensors = (cu_seqlens_q, cu_seqlens_ori_kv, cu_seqlens_cmp_kv, seqused_q, seqused_kv)
+    dev = torch.device(device) if device is not None else None
+    if (dev is not None and dev.type == "cuda"
+            and all(isinstance(t, torch.Tensor) for t in tensors if t is not None)
+            and any(t is not None for t in tensors)
+            and all(t.is_cuda for t in tensors if t is not None)):
+        tdev = next(t.device for t in tensors if t is not None)
+        if all(t.device == tdev for t in tensors if t is not None) and (dev.index is None or dev.index == tdev.index):
+            return _metadata_device(tdev, tensors, num_heads_q=num_heads_q, num_heads_kv=num_heads_kv,
+                                    head_dim=head_dim, batch_size=batch_size, max_seqlen_q=max_seqlen_q,
+                                    max_seqlen_kv=max_seqlen_kv, ori_topk=ori_topk, cmp_topk=cmp_topk,
+                                    cmp_ratio=cmp_ratio, ori_mask_mode=ori_mask_mode,
+                                    cmp_mask_mode=cmp_mask_mode, ori_win_left=ori_win_left,
+                                    ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
+                                    has_ori_kv=has_ori_kv, has_cmp_kv=has_cmp_kv, aic_core_num=aic_core_num,
+                                    aiv_core_num=aiv_core_num)
     keep = []
-    p = _lib.SasMetaParams()
-    p.num_heads_q, p.num_heads_kv, p.head_dim = int(num_heads_q), int(num_heads_kv), int(head_dim)
-    p.batch_size, p.max_seqlen_q, p.max_seqlen_kv = int(batch_size), int(max_seqlen_q), int(max_seqlen_kv)
-    p.ori_topk, p.cmp_topk, p.cmp_ratio = int(ori_topk), int(cmp_topk), int(cmp_ratio)
-    p.ori_mask_mode, p.cmp_mask_mode = int(ori_mask_mode), int(cmp_mask_mode)
-    p.ori_win_left, p.ori_win_right = int(ori_win_left), int(ori_win_right)
-    lq, lkv = str(layout_q).encode(), str(layout_kv).encode()
-    p.layout_q, p.layout_kv = lq, lkv
-    p.has_ori_kv, p.has_cmp_kv = int(bool(has_ori_kv)), int(bool(has_cmp_kv))
-    p.aic_core_num, p.aiv_core_num = int(aic_core_num), int(aiv_core_num)
+    p = _params(num_heads_q=num_heads_q, num_heads_kv=num_heads_kv, head_dim=head_dim, batch_size=batch_size,
+                max_seqlen_q=max_seqlen_q, max_seqlen_kv=max_seqlen_kv, ori_topk=ori_topk, cmp_topk=cmp_topk,
+                cmp_ratio=cmp_ratio, ori_mask_mode=ori_mask_mode, cmp_mask_mode=cmp_mask_mode,
+                ori_win_left=ori_win_left, ori_win_right=ori_win_right, layout_q=layout_q, layout_kv=layout_kv,
+                has_ori_kv=has_ori_kv, has_cmp_kv=has_cmp_kv, aic_core_num=aic_core_num,
+                aiv_core_num=aiv_core_num, keep=keep)
     for name, t in (("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_ori_kv", cu_seqlens_ori_kv),
                     ("cu_seqlens_cmp_kv", cu_seqlens_cmp_kv), ("seqused_q", seqused_q),
                     ("seqused_kv", seqused_kv)):

@@ -79,6 +79,20 @@ typedef struct SasMetaParams {
 int sas_metadata_v1(const SasMetaParams* p, int32_t* out /* [SAS_META_SIZE] */);
 
 /*
+ * The same schedule computed on the GPU, for callers whose sequence lengths
+ * live there: no device -> host copy and no synchronisation, where the
+ * reference reads them back to the host for it (api.py:210, 336, 361;
+ * metadata.py:1018-1086). The SasMetaParams arrays (cu_seqlens_*,
+ * seqused_*) are DEVICE pointers with their host-side lengths; `out` is a
+ * device int32[SAS_META_SIZE], written by one launch on `stream`. Bit-exact
+ * with sas_metadata_v1. At most 1024 batches (SAS_EINVAL beyond). A call
+ * whose schedule sas_metadata_v1 rejects with SAS_EINVAL on the data (a row
+ * scan that does not end), or whose batches hold more than 2^22 query rows in
+ * all, leaves out[0] = -1 (no valid schedule has a negative core flag).
+ */
+int sas_metadata_device_v1(const SasMetaParams* p, int32_t* out /* device [SAS_META_SIZE] */, void* stream);
+
+/*
  * Forward arguments; the device tensors of the reference kernel callable
  * (sparse_attn_sharedkv_tilelang/kernel.py:158-178) plus dims and strides.
  * q/out are flat token-major [T, H, D] / [T, H, DV]; q_prefix/act_q give each

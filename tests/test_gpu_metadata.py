@@ -1,0 +1,81 @@
+"""Device scheduler (``sas_metadata_device_v1``, through
+``sparse_attn_sharedkv_metadata(..., device="cuda")`` with device-resident
+sequence lengths) against the reference's recorded vectors and the host
+scheduler, bit for bit."""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+
+from dsv4_amd import cases as C
+from dsv4_amd.metadata import sparse_attn_sharedkv_metadata
+from test_metadata import FIX, TENSOR_KEYS, _expected, _fuzz_kwargs, _kw
+
+pytestmark = pytest.mark.gpu
+
+
+def _on_device(kw):
+    out = dict(kw)
+    for k in TENSOR_KEYS:
+        if isinstance(out.get(k), torch.Tensor):
+            out[k] = out[k].cuda()
+    out["device"] = "cuda"
+    return out
+
+
+@pytest.mark.parametrize("case", FIX["cases"], ids=[c["name"] for c in FIX["cases"]])
+def test_device_scheduler_matches_reference_vectors(case):
+    got = sparse_attn_sharedkv_metadata(**_on_device(_kw(case["kwargs"])))
+    assert got.is_cuda and got.dtype == torch.int32
+    assert got.cpu().tolist() == _expected(case)
+
+
+def test_device_scheduler_matches_host_fuzz():
+    rnd = random.Random(20261)
+    n_dev = 0
+    for i in range(400):
+        kw = _fuzz_kwargs(rnd)
+        try:
+            host = sparse_attn_sharedkv_metadata(**kw).tolist()
+        except ValueError:
+            host = None   # a row scan the host rejects: the device marks out[0] = -1
+        dev = sparse_attn_sharedkv_metadata(**_on_device(kw)).cpu().tolist()
+        if host is None:
+            assert dev[0] == -1, f"fuzz case {i}: {kw}"
+        else:
+            assert dev == host, f"fuzz case {i}: {kw}"
+        n_dev += any(isinstance(kw.get(k), torch.Tensor) for k in TENSOR_KEYS)
+    assert n_dev > 300   # most cases pass lengths, so they ran on the device
+
+
+@pytest.mark.parametrize("name", ["C2", "C3", "scfa_prefill"])
+def test_device_scheduler_at_benchmark_shapes(name):
+    """The decode and prefill workloads (C3: 4096 query rows; the
+    reference's 8K prefill: rows past the 6144 kept in LDS are computed by
+    the assigning thread): same rows as the host, and the launch time."""
+    cfg = C.CONFIGS.get(name) or C.REF_SCENARIOS[name]
+    ql, kl = C.seq_lengths(cfg)
+    cu = [0]
+    for x in ql:
+        cu.append(cu[-1] + x)
+    kw = dict(num_heads_q=cfg.H, num_heads_kv=1, head_dim=cfg.D,
+              cu_seqlens_q=torch.tensor(cu, dtype=torch.int32),
+              seqused_kv=torch.tensor(kl, dtype=torch.int32), batch_size=cfg.B,
+              max_seqlen_q=max(ql), max_seqlen_kv=max(kl), layout_q="TND",
+              has_cmp_kv=cfg.scenario >= 2, cmp_ratio=cfg.cmp_ratio if cfg.scenario >= 2 else -1,
+              cmp_topk=cfg.K if cfg.scenario == 3 else 0)
+    host = sparse_attn_sharedkv_metadata(**kw).tolist()
+    dkw = _on_device(kw)
+    dev = sparse_attn_sharedkv_metadata(**dkw)
+    assert dev.cpu().tolist() == host
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        sparse_attn_sharedkv_metadata(**dkw)
+    e1.record()
+    torch.cuda.synchronize()
+    print(f"[metadata] {name}: {sum(ql)} query rows, device schedule {e0.elapsed_time(e1) * 100:.1f} us per call",
+          flush=True)

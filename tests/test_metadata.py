@@ -5,9 +5,12 @@ inputs, and the reference suite's invariants
 
 from __future__ import annotations
 
+import ctypes
 import json
 import os
 import random
+import shutil
+import subprocess
 
 import pytest
 import torch
@@ -178,3 +181,47 @@ def test_scheduler_device_argument():
                                        batch_size=1, max_seqlen_q=1, max_seqlen_kv=300,
                                        device="cpu")
     assert md.device.type == "cpu" and md[0] == 1
+
+
+def test_device_arithmetic_width_matches_host(tmp_path):
+    """The device scheduler computes token ranges in 64-bit integers with the
+    INT64_MAX bounds saturated at 2^40; the host in 128-bit ones. The shared
+    schedule code (dsv4_amd/csrc/sas_sched.h) gives the same rows either way
+    on 20000 seeded inputs (tests/c/sched_width_check.cpp: windows around and
+    far beyond 2^40, every mask mode and layout, empty batches)."""
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    exe = tmp_path / "sched_width_check"
+    subprocess.run([gxx, "-O2", "-std=c++17", "-o", str(exe), os.path.join(HERE, "c", "sched_width_check.cpp")],
+                   check=True)
+    r = subprocess.run([str(exe), "20000", "2026"], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0 and r.stdout.strip() == "ok 20000", r.stdout + r.stderr
+
+
+def _dev_params(**over):
+    from dsv4_amd import _lib
+    p = _lib.SasMetaParams()
+    p.num_heads_q, p.num_heads_kv, p.head_dim = 64, 1, 576
+    p.batch_size, p.max_seqlen_q, p.max_seqlen_kv = 1, 1, 100
+    p.cmp_ratio, p.ori_mask_mode, p.ori_win_left = 4, 4, 127
+    p.layout_q, p.layout_kv = b"BSND", b"PA_ND"
+    p.aic_core_num, p.aiv_core_num = 24, 48
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("over,needle", [
+    (dict(num_heads_kv=0), "num_heads_kv"),
+    (dict(aic_core_num=0), "aic_core_num"),
+    (dict(batch_size=1025), "at most 1024 batches"),
+    (dict(batch_size=-1), "negative batch"),
+], ids=["heads", "cores", "batches", "negative"])
+def test_device_scheduler_rejects_before_device_work(over, needle):
+    from dsv4_amd import _lib
+    fake = 1 << 40   # never dereferenced: validation fails first
+    rc = _lib.lib().sas_metadata_device_v1(ctypes.byref(_dev_params(**over)), ctypes.c_void_p(fake), None)
+    assert rc == _lib.SAS_EINVAL
+    assert needle in _lib.lib().sas_last_error().decode()
+    assert _lib.lib().sas_metadata_device_v1(None, ctypes.c_void_p(fake), None) == _lib.SAS_EINVAL
