@@ -37,6 +37,9 @@ constexpr int kBwdRows = 16;   // rows per chunk (= lanes per head)
 #ifndef SAS_BWD_NG
 #define SAS_BWD_NG 2   // 16-head groups per workgroup when H is a multiple of 32 (1 or 2)
 #endif
+#ifndef SAS_BWD64
+#define SAS_BWD64 1    // 1: 64-head workgroups (sas_bwd64_kernel) when H is a multiple of 64
+#endif
 
 struct BwdParams {
   FwdParams f;
@@ -296,6 +299,255 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
   }
 }
 
+// 64-head workgroups (H a multiple of 64): 8 waves, wave w = 2 g + hh holds
+// head group g (16 heads) and channel half hh. The dkv atomics are one per
+// (token, row, channel) for all 64 heads, half those of 32-head workgroups,
+// and the row-gradient atomics bound the backward. The q / dO tiles of 64
+// heads (141 KB) do not fit beside the row tile in LDS, so q lives in
+// registers, spread over the waves: each wave holds its head group's Q^T
+// fragments for its half of the S = K Q^T channels and, for its dkv channel
+// tiles (w, w + 8, ...), the q B-operands of all four head groups; dO stays
+// in LDS. Per 16-row chunk: each wave sums its channel half of S^T and dP^T
+// (16x16x32 MFMA), the pair adds the halves through LDS (own + other, the
+// same bits in both waves), P and scale dS go to the (P, dS) table, then dq
+// over the wave's head group and channel half, and the dkv tiles (dS^T . Q +
+// P^T . dO summed over the four groups) with one atomic add per value.
+template <int D, typename QT>
+__global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
+  constexpr int NT = 512, NHD = 64;
+  constexpr int CH = D / 8;                // 16-byte chunks per row
+  constexpr int KS = D * 2 + 16;           // row tile stride (bytes)
+  constexpr int QSTR = D * 2 + 16;         // staged q row stride (bytes)
+  constexpr int OS = kDV * 2 + 16;         // dO row stride (bytes)
+  constexpr int KSH = D / 64;              // S k-steps (32 channels) per channel half
+  constexpr int VSH = kDV / 64;            // dP k-steps per channel half
+  constexpr int NCT = D / 16;              // 16-channel tiles
+  constexpr int MT = (NCT + 7) / 8;        // dkv tiles per wave (at most)
+  constexpr int DQT = NCT / 2;             // dq tiles per wave (its channel half)
+  static_assert(NCT % 2 == 0 && KSH * 2 * 32 == D, "channel halves");
+  // q is staged here for the register loads, then dO takes the space
+  __shared__ __attribute__((aligned(16))) uint8_t lds_qo[NHD * QSTR];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_k[kBwdRows * KS];
+  __shared__ float lds_pd[kBwdRows][NHD][2];   // (P, scale dS) per row and head
+  __shared__ float lds_hd[NHD][2];             // per head: Delta, lse (log2 units)
+  __shared__ f32x4 lds_x[8][2][64];            // S^T / dP^T channel halves per wave
+
+  const FwdParams& p = bp.f;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int item = item_index(p);
+  if (item < 0) return;
+  Tok k = item_of(p, item);
+  resolve<256, D * 2>(p, k, tid, lane, wave, [] {});
+  const int g = wave >> 1, hh = wave & 1;
+  const int c16 = lane & 15, g4 = lane >> 4;
+  const int t = k.t, h0 = k.hg * NHD;
+  if (k.padded) return;   // dq stays zero (the caller zeroes it)
+
+  // Delta = dO . O: 8 threads per head, 64 channels each, 8-lane sums
+  {
+    const int hd = tid >> 3, part = tid & 7, hq = h0 + hd;
+    const uint32_t* dog = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(bp.dout) +
+                                                            ((size_t)t * p.H + hq) * kDV) + part * 32;
+    const uint32_t* og = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(bp.out) +
+                                                           ((size_t)t * p.H + hq) * kDV) + part * 32;
+    float dpart = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) dpart = dot2<QT>(dog[i], og[i], dpart);
+    dpart += __shfl_xor(dpart, 1);
+    dpart += __shfl_xor(dpart, 2);
+    dpart += __shfl_xor(dpart, 4);
+    const float lse2 = p.lse[(size_t)t * p.H + hq] * kLog2e;
+    if (part == 0) {
+      lds_hd[hd][0] = dpart;
+      lds_hd[hd][1] = lse2;
+      if (k.sp == 0) {
+        const float psink = __builtin_amdgcn_exp2f(p.sinks[hq] * kLog2e - lse2);
+        atomicAdd(bp.d_sinks + hq, -psink * dpart);
+      }
+    }
+  }
+  // col4(base, stride, ct): the 16-bit values of rows 4 g4 .. 4 g4 + 3 of
+  // `base` at channel 16 ct + c16, packed as an MFMA operand, by one
+  // transposed read (rows padded by 16 bytes)
+  auto col4 = [&](const uint8_t* base, int stride, int ct) {
+    const uint8_t* a = base + (4 * g4 + (c16 >> 2)) * stride + (ct * 16 + 4 * (c16 & 3)) * 2;
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a)));
+  };
+  // q of the 64 heads staged in LDS, read into registers: qs = this wave's
+  // Q^T fragments (head 16 g + c16, channels 32 (hh KSH + ks) + 8 g4 ..),
+  // qk[m][gg] = q of heads 16 gg + 4 g4 .. + 3 at channel 16 (wave + 8 m) + c16
+  uint4 qs[KSH];
+  uint2 qk[MT][4];
+  {
+    const uint4* qg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.q) +
+                                                     ((size_t)t * p.H + h0) * D);
+    for (int i = tid; i < NHD * CH; i += NT)
+      *reinterpret_cast<uint4*>(lds_qo + (i / CH) * QSTR + (i % CH) * 16) = qg[i];
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < KSH; ++ks)
+      qs[ks] = *reinterpret_cast<const uint4*>(lds_qo + (16 * g + c16) * QSTR + ((hh * KSH + ks) * 32 + 8 * g4) * 2);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int ct = wave + 8 * m;
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg)
+        qk[m][gg] = ct < NCT ? col4(lds_qo + gg * 16 * QSTR, QSTR, ct) : make_uint2(0, 0);
+    }
+    __syncthreads();   // every wave has its q before dO overwrites it
+    const uint4* ds = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(bp.dout) +
+                                                     ((size_t)t * p.H + h0) * kDV);
+    for (int i = tid; i < NHD * kDV / 8; i += NT)
+      *reinterpret_cast<uint4*>(lds_qo + (i / (kDV / 8)) * OS + (i % (kDV / 8)) * 16) = ds[i];
+  }
+  const float scale = p.scale_log2 / kLog2e;
+  const uint64_t ori_lo = reinterpret_cast<uint64_t>(p.ori_kv);
+  const uint64_t ori_n = (uint64_t)p.ori_nblocks * p.ori_bs * (D * 2);
+  const uint64_t cmp_lo = reinterpret_cast<uint64_t>(p.cmp_kv);
+  f32x4 dqt[DQT];
+#pragma unroll
+  for (int j = 0; j < DQT; ++j) dqt[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Row chunks double-buffered through registers, as in the 32-head kernel
+  constexpr int NLD = (kBwdRows * CH + NT - 1) / NT;
+  uint4 rbuf[NLD];
+  auto load_rows = [&](int c0n) {
+    const int nrn = min(kBwdRows, k.nvalid - c0n);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      const int i = tid + NT * j;
+      if (i < kBwdRows * CH) {
+        const int r = i / CH, c = i - r * CH;
+        rbuf[j] = *reinterpret_cast<const uint4*>(lds_rows[c0n + min(r, nrn - 1)] + c * 16);
+      }
+    }
+  };
+  if (k.nvalid > 0) load_rows(0);
+
+  for (int c0 = 0; c0 < k.nvalid; c0 += kBwdRows) {
+    const int nr = min(kBwdRows, k.nvalid - c0);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      const int i = tid + NT * j;
+      if (i < kBwdRows * CH) {
+        const int r = i / CH, c = i - r * CH;
+        *reinterpret_cast<uint4*>(lds_k + r * KS + c * 16) = rbuf[j];
+      }
+    }
+    __syncthreads();   // the chunk (and, the first time, dO) in LDS
+    if (c0 + kBwdRows < k.nvalid) load_rows(c0 + kBwdRows);
+    // this wave's channel half of S^T = K . Q^T and dP^T = V . dO^T for its
+    // head group: A = 8 channels of key c16, B = the same channels of head c16
+    {
+      f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f}, dacc = sacc;
+      const uint8_t* kb = lds_k + c16 * KS + g4 * 16;
+      const uint8_t* ob = lds_qo + (16 * g + c16) * OS + g4 * 16;
+#pragma unroll
+      for (int ks = 0; ks < KSH; ++ks)
+        sacc = mfma32k<QT>(*reinterpret_cast<const uint4*>(kb + (hh * KSH + ks) * 64), qs[ks], sacc);
+#pragma unroll
+      for (int vs = 0; vs < VSH; ++vs) {
+        const int off = (hh * VSH + vs) * 64;
+        dacc = mfma32k<QT>(*reinterpret_cast<const uint4*>(kb + off), *reinterpret_cast<const uint4*>(ob + off), dacc);
+      }
+      lds_x[wave][0][lane] = sacc;
+      lds_x[wave][1][lane] = dacc;
+      __syncthreads();
+      sacc += lds_x[wave ^ 1][0][lane];
+      dacc += lds_x[wave ^ 1][1][lane];
+      // lane (g4, c16): keys 4 g4 .. + 3 of head 16 g + c16; one wave of the
+      // pair writes their P and scale dS
+      if (hh == 0) {
+        const int hd = 16 * g + c16;
+        const float dl = lds_hd[hd][0], l2 = lds_hd[hd][1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = 4 * g4 + i;
+          float pr = 0.f, dsr = 0.f;
+          if (key < nr) {
+            pr = __builtin_amdgcn_exp2f(sacc[i] * p.scale_log2 - l2);
+            dsr = pr * (dacc[i] - dl) * scale;
+          }
+          lds_pd[key][hd][0] = pr;
+          lds_pd[key][hd][1] = dsr;
+        }
+      }
+    }
+    __syncthreads();
+    // dq[head][ch] += dS[head][key] . K[key][ch] over this wave's head group
+    // and channel half (A = keys 4 g4 .. + 3 of head c16; B = the same keys
+    // of channel 16 ct + c16, rows past nr carry dS = 0)
+    {
+      const int hd = 16 * g + c16;
+      uint2 a_dq;
+      a_dq.x = pack2<QT>(lds_pd[4 * g4][hd][1], lds_pd[4 * g4 + 1][hd][1]);
+      a_dq.y = pack2<QT>(lds_pd[4 * g4 + 2][hd][1], lds_pd[4 * g4 + 3][hd][1]);
+#pragma unroll
+      for (int j = 0; j < DQT; ++j) dqt[j] = mfma16k<QT>(a_dq, col4(lds_k, KS, hh * DQT + j), dqt[j]);
+    }
+    // dkv rows of the chunk, tiles ct = wave + 8 m: dK[key][ch] = sum over
+    // the four head groups of dS[key][head] . Q[head][ch] (+ P[key][head] .
+    // dO[head][ch] for ch < 512); A = 4 heads (4 g4 .. + 3) of key c16 from
+    // the table, rounded to the query dtype; lane (g4, c16) then holds keys
+    // 4 g4 .. + 3 of channel 16 ct + c16 and adds them to the fp32 gradients
+    {
+      uint2 a_ds[4], a_p[4];
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) {
+        const int hb = gg * 16 + 4 * g4;
+        a_ds[gg].x = pack2<QT>(lds_pd[c16][hb][1], lds_pd[c16][hb + 1][1]);
+        a_ds[gg].y = pack2<QT>(lds_pd[c16][hb + 2][1], lds_pd[c16][hb + 3][1]);
+        a_p[gg].x = pack2<QT>(lds_pd[c16][hb][0], lds_pd[c16][hb + 1][0]);
+        a_p[gg].y = pack2<QT>(lds_pd[c16][hb + 2][0], lds_pd[c16][hb + 3][0]);
+      }
+      float* grow[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = 4 * g4 + i;
+        const uint64_t a = lds_rows[c0 + min(key, nr - 1)];
+        grow[i] = key < nr ? (a - ori_lo < ori_n ? bp.d_ori + (a - ori_lo) / (D * 2) * D
+                                                 : bp.d_cmp + (a - cmp_lo) / (D * 2) * D)
+                           : nullptr;
+      }
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const int ct = wave + 8 * m;
+        if (ct >= NCT) break;   // wave-uniform
+        const int ch = ct * 16 + c16;
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+          acc = mfma16k<QT>(a_ds[gg], qk[m][gg], acc);
+          if (ct < kDV / 16) acc = mfma16k<QT>(a_p[gg], col4(lds_qo + gg * 16 * OS, OS, ct), acc);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (grow[i]) atomicAdd(grow[i] + ch, acc[i]);
+      }
+    }
+    __syncthreads();
+  }
+  // one split: the workgroup owns its heads' dq; several: each adds its share
+  float* dqb = bp.dq + ((size_t)t * p.H + h0 + 16 * g + 4 * g4) * D + c16;
+#pragma unroll
+  for (int j = 0; j < DQT; ++j) {
+    const int ct = hh * DQT + j;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (p.nsplit == 1) dqb[(size_t)i * D + ct * 16] = dqt[j][i];
+      else atomicAdd(dqb + (size_t)i * D + ct * 16, dqt[j][i]);
+    }
+  }
+}
+
+template <int D, typename QT>
+int launch_bwd64(const BwdParams& bp, int nblocks, hipStream_t st) {
+  hipLaunchKernelGGL((sas_bwd64_kernel<D, QT>), dim3(nblocks), dim3(512), 0, st, bp);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(SAS_ELAUNCH, "sas_bwd64 launch: %s", hipGetErrorString(e));
+  return SAS_OK;
+}
+
 template <int D, typename QT, int NG>
 int launch_bwd(const BwdParams& bp, int nblocks, hipStream_t st) {
   hipLaunchKernelGGL((sas_bwd_kernel<D, QT, NG>), dim3(nblocks), dim3(256 * NG), 0, st, bp);
@@ -365,14 +617,18 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   fp.scale_log2 = a->softmax_scale * kLog2e;
   // KV splits: the caller's count, else enough (token, head group, split)
   // workgroups for two per CU, each split at least 64 slots
-  // two 16-head groups per workgroup when H allows (half the dkv atomics)
-  const int ng = a->H % 32 == 0 ? SAS_BWD_NG : 1;
+  // 64 heads per workgroup when H allows, else two 16-head groups (each
+  // doubling halves the dkv atomics)
+  const bool b64 = SAS_BWD64 && a->H % 64 == 0;
+  const int ng = b64 ? 4 : a->H % 32 == 0 ? SAS_BWD_NG : 1;
   fp.nhg = (int)a->H / (16 * ng);
   int ns = a->num_splits;
   if (ns <= 0) {
-    // enough (token, head groups, split) workgroups for 8 waves per CU
+    // enough (token, head groups, split) workgroups for 8 waves per CU (one
+    // 8-wave workgroup per CU: 64 heads; 32 heads; two of 4 waves: 16 heads)
     const long long items = a->T * fp.nhg;
-    const long long want = (2 * device_cus() / ng + items - 1) / items;
+    const long long wgs = ng == 1 ? 2LL * device_cus() : (long long)device_cus();
+    const long long want = (wgs + items - 1) / items;
     ns = (int)std::min<long long>(want, (nslots + 63) / 64);
   }
   ns = std::max(1, std::min(ns, 64));
@@ -394,6 +650,11 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   bp.d_sinks = ba->d_sinks;
   const int nblocks = (int)((a->T + kXcds - 1) / kXcds) * fp.nhg * fp.nsplit * kXcds;
   hipStream_t st = (hipStream_t)stream;
+  if (b64) {
+    if (a->q_dtype == SAS_DT_BF16)
+      return a->D == 576 ? launch_bwd64<576, __bf16>(bp, nblocks, st) : launch_bwd64<512, __bf16>(bp, nblocks, st);
+    return a->D == 576 ? launch_bwd64<576, _Float16>(bp, nblocks, st) : launch_bwd64<512, _Float16>(bp, nblocks, st);
+  }
   if (a->q_dtype == SAS_DT_BF16)
     return a->D == 576 ? launch_bwd_ng<576, __bf16>(bp, ng, nblocks, st)
                        : launch_bwd_ng<512, __bf16>(bp, ng, nblocks, st);
