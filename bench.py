@@ -385,7 +385,8 @@ def bench_backward(dec_inp, pre_inp, atomic_peak=None):
     rate is far below the MFMA peak)."""
     from dsv4_amd import cases
     from dsv4_amd.api import prepare_sparse_attn_sharedkv_backward, sparse_attn_sharedkv
-    res = {"kernel": "sas_bwd_kernel (MFMA scores, dq and dkv; fp32 atomics for dkv)",
+    res = {"kernel": "sas_bwd64_kernel (64-head workgroups, q in registers; MFMA scores, dq and dkv; "
+                     "fp32 atomics for dkv); sas_bwd_kernel for H not a multiple of 64",
            "flop_per_pair_head": BWD_FLOP_PER_PAIR_HEAD}
     for key, inp, steps in (("decode", dec_inp, 50), ("prefill", pre_inp, 3)):
         if inp is None:
@@ -400,7 +401,7 @@ def bench_backward(dec_inp, pre_inp, atomic_peak=None):
         pairs = cases.gathered_rows(inp)
         flop = pairs * inp.cfg.H * BWD_FLOP_PER_PAIR_HEAD
         tfl = flop / (us * 1e-6) / 1e12
-        hpw = 32 if inp.cfg.H % 32 == 0 else 16
+        hpw = 64 if inp.cfg.H % 64 == 0 else 32 if inp.cfg.H % 32 == 0 else 16
         D = inp.q.shape[-1]
         atomics = pairs * (inp.cfg.H // hpw) * D
         rate = atomics / (us * 1e-6) / 1e9

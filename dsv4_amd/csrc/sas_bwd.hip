@@ -13,18 +13,19 @@
 //   dkv_j += scale dS_j q  +  [P_j dO, 0]   (summed over heads and tokens)
 //   dsink += -P_sink Delta                   (the sink's value row is zero)
 //
-// One workgroup per (token, head group, KV split): 32 heads (8 waves, two
-// 16-head groups sharing the row tile) when H is a multiple of 32, else 16
-// heads (4 waves). With few tokens the token's key slots are split over
-// several workgroups (as in the forward), which then add their dq shares
-// atomically. Thread (h, part) sums Delta = dO . O over D / 16 channels of
-// head h (16 lanes, DPP sums). Rows
-// stream through LDS in chunks of 16 (the next chunk's loads in flight in
-// registers): S^T and dP^T are 16x16x32 MFMAs (the first wave of each head
-// group computes the group's 16 x 16 tile), P and dS go to an LDS table, then dq (dS . K, accumulated across chunks in
-// registers) and the chunk's dkv rows (dS^T . Q + P^T . dO, summed over the
-// heads, added to the fp32 gradient cache rows with atomics) are 16x16x16
-// MFMAs per 16-channel tile.
+// One workgroup per (token, head group, KV split). The fp32 atomic adds of
+// the row gradients, one per (token, row, head group, channel), bound the
+// backward, so head groups are as wide as registers and LDS allow: 64 heads
+// (sas_bwd64_kernel, q in registers) when H is a multiple of 64, else 32
+// (8 waves, two 16-head groups sharing the row tile) or 16 heads (4 waves)
+// with q and dO in LDS (sas_bwd_kernel). With few tokens the token's key
+// slots are split over several workgroups (as in the forward), which then add
+// their dq shares atomically. Rows stream through LDS in chunks of 16 (the
+// next chunk's loads in flight in registers): S^T and dP^T are 16x16x32
+// MFMAs, P and dS go to an LDS table, then dq (dS . K, accumulated across
+// chunks in registers) and the chunk's dkv rows (dS^T . Q + P^T . dO, summed
+// over the heads, added to the fp32 gradient cache rows with atomics) are
+// 16x16x16 MFMAs per 16-channel tile.
 
 #include <type_traits>
 
