@@ -368,6 +368,33 @@ struct Fwd {
       for (int i = 0; i < C::NTL; ++i) acc[i] *= alpha;
     }
   }
+  // smax_a for the pipelined 8-wave loop, written without branches so it can
+  // sit between the next step's QK^T MFMAs: every key goes through the mask,
+  // and the reference max and l move by alpha = exp2(m_run - m_new) (1 when
+  // no head rises past the lazy threshold). Returns whether O must be scaled
+  // by alpha before the step's P.V (the caller does it after the MFMAs).
+  __device__ __forceinline__ bool smax_front(const f32x4 (&sacc)[C::MT], int step, float (&sv)[C::MT][4],
+                                             float& alpha) {
+    constexpr int MT = C::MT;
+    const int nk = min(C::TR, nrows - step * C::TR);
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = mt * 16 + g * 4 + j;
+        const float x = key < nk ? sacc[mt][j] * p.scale_log2 : -INFINITY;
+        sv[mt][j] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    mloc = rows_max(mloc);
+    const bool r = __ballot(mloc > m_run + kLazyLog2) != 0;
+    const float m_new = r ? fmaxf(m_run, mloc) : m_run;
+    alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    l_run *= alpha;
+    m_run = m_new;
+    return r;
+  }
   static constexpr int kSmaxB = C::MT * 4 + 2;
   __device__ __forceinline__ void smax_b(int e, float (&sv)[C::MT][4], float& lsum, uint32_t (&pk)[2 * C::MT]) {
     constexpr int MT = C::MT;
@@ -720,25 +747,41 @@ struct Fwd {
     // every wave has finished P.V of step it - 1 (slot Jf is free)
     wait_vm<0>();
     lds_barrier();
-    f32x4 sc[C::MT], dummy[C::MT];
+    f32x4 sc[C::MT];
     xs_read(it & 1, sc);
-    float sv[C::MT][4], lsum = 0.f;
+    float sv[C::MT][4], lsum = 0.f, alpha = 1.f;
     uint32_t pk[2 * C::MT];
-    smax_a<false>(sc, dummy, it, sv);
-    const bool more = it + 2 < nsteps;
-    Dma d;
-    if (more) prep(d, Jf, it + 2);
+    bool resc;
     if (nxt) {
+      // The DMA of step it + 2 goes out unconditionally: past the last step
+      // it re-reads the last row into slot Jf, which no later step reads (the
+      // last iteration waits for it), so the QK^T loop has no branch. The
+      // softmax front of step it (S read back above, max, reference move)
+      // runs between the first MFMAs. (Its exps and packing, which the
+      // compiler places after the MFMAs, measured slower when forced between
+      // them: the other wave on the SIMD overlaps them already.)
+      Dma d;
+      prep(d, Jf, it + 2);
       f32x4 sn[C::MT], so[C::MT];
-      qk<true>(slot(Jn), sn, so, [&](int o) { if (more) fire(d, o); }, [&](int ks) {
-        if (ks < kSmaxB) smax_b(ks, sv, lsum, pk);
+      qk<true>(slot(Jn), sn, so, [&](int o) { fire(d, o); }, [&](int ks) {
+        if (ks == 0) resc = smax_front(sc, it, sv, alpha);
+        else if (ks - 1 < kSmaxB) smax_b(ks - 1, sv, lsum, pk);
       });
 #pragma unroll
-      for (int e = C::KSQ; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
+      for (int e = C::KSQ - 1; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
       xs_write((it + 1) & 1, sn);
     } else {
+      // (an empty asm on the scores keeps the compiler from hoisting this
+      // copy of the softmax above the branch)
+#pragma unroll
+      for (int mt = 0; mt < C::MT; ++mt) asm volatile("" : "+v"(sc[mt]));
+      resc = smax_front(sc, it, sv, alpha);
 #pragma unroll
       for (int e = 0; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
+    }
+    if (resc) {
+#pragma unroll
+      for (int i = 0; i < C::NTL; ++i) acc[i] *= alpha;
     }
     pv(slot(J), pk, [](int) {});
   }
