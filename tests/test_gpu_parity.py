@@ -162,6 +162,18 @@ def test_wave_layout_does_not_change_result(hw, waves):
     _check_baseline(out, lse, ref_out, ref_lse, f"C2 hw{hw} waves{waves}")
 
 
+@pytest.mark.parametrize("splits", [1, 2, 3, 5, 9])
+def test_two_key_group_pipeline_ragged_rows(splits):
+    """32-head, 8-wave workgroups (two key-groups of 16-row steps, the
+    batched-decode loop) on 1 to a few hundred rows per workgroup: key-groups
+    of unequal step counts, an empty second key-group, partial last steps,
+    one-step and two-step key-groups."""
+    inp = _small(B=4, H=64, q_lens=[1, 3, 2, 5], kv_lens=[1, 40, 700, 3000], K=200)
+    out, lse, ns = _run(inp, num_splits=splits, head_waves=2, waves=8)
+    ref_out, ref_lse = _oracle(inp)
+    _check_baseline(out, lse, ref_out, ref_lse, f"hw2 waves8 splits {splits}->{ns}")
+
+
 # ---------------------------------------------------------------------------
 # the reference suite's scenarios (same data as its _build_case)
 # ---------------------------------------------------------------------------
