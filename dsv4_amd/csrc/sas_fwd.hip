@@ -40,6 +40,9 @@
 #ifndef SAS_PFK
 #define SAS_PFK 3   // K operand k-steps read ahead (32-row steps)
 #endif
+#ifndef SAS_KG2_SPLIT_MERGE
+#define SAS_KG2_SPLIT_MERGE 1   // two key-groups each merge and store half the channels
+#endif
 #ifndef SAS_PFV
 #define SAS_PFV 4   // V^T operand channel tiles read ahead (32-row steps)
 #endif
@@ -879,6 +882,103 @@ __device__ __forceinline__ void epilogue(const FwdParams& p, const Tok& k, int t
   const bool split = p.nsplit > 1;
   const int t = k.t;
   float M = m_run, L = l_run;
+#if SAS_KG2_SPLIT_MERGE
+  if constexpr (KW == 2 && CS == 2) {
+    // Two key-groups, channel-split waves (the 32-head decode workgroup):
+    // the two waves holding the same 16 heads x 256 channels (one per
+    // key-group) each own half of those channels. Each passes the other
+    // its scaled O for the other half through LDS, adds what it receives
+    // (same sum as one wave adding both: own + other is commutative), and
+    // stores its half, so the merge, the staging and the stores run on all
+    // eight waves.
+    constexpr int HT = NTL / 2;                      // tiles per owned half
+    constexpr int XS = 16 * (HT * 16 + 4);           // floats per passed half (+4 pad per head)
+    static_assert(NW * XS * 4 <= kLdsRows * kChunksMax * 16, "merge buffers fit");
+    if (g == 0) { lds_ml[wave][0][c16] = m_run; lds_ml[wave][1][c16] = l_run; }
+    __syncthreads();
+    const int pw = (1 - kw) * WK + jw;               // the partner wave
+    const float m0 = lds_ml[jw][0][c16], m1 = lds_ml[WK + jw][0][c16];
+    M = fmaxf(m0, m1);
+    const float w0 = m0 == -INFINITY ? 0.f : exp2f(m0 - M), w1 = m1 == -INFINITY ? 0.f : exp2f(m1 - M);
+    L = w0 * lds_ml[jw][1][c16] + w1 * lds_ml[WK + jw][1][c16];
+    const float w_self = kw == 0 ? w0 : w1;
+    // o: the owned half (tiles HT kw ..), selected without indexing acc by a
+    // runtime value (which would move acc to scratch memory)
+    f32x4 o[HT];
+    {
+      float* xb = reinterpret_cast<float*>(lds_ring) + pw * XS;
+#pragma unroll
+      for (int i = 0; i < HT; ++i) {
+        const f32x4 lo = acc[i] * w_self, hi = acc[HT + i] * w_self;
+        o[i] = kw == 0 ? lo : hi;
+        *reinterpret_cast<f32x4*>(xb + c16 * (HT * 16 + 4) + i * 16 + g * 4) = kw == 0 ? hi : lo;
+      }
+    }
+    __syncthreads();
+    {
+      const float* xb = reinterpret_cast<const float*>(lds_ring) + wave * XS;
+#pragma unroll
+      for (int i = 0; i < HT; ++i) o[i] += *reinterpret_cast<const f32x4*>(xb + c16 * (HT * 16 + 4) + i * 16 + g * 4);
+    }
+    const int chw = ch0 + kw * HT * 16;              // this wave's first stored channel
+    const int h0 = k.hg * nhead_wg + hw * 16;
+    constexpr int PES = sizeof(PartT<QT>);
+    int e2 = 0;
+    if (split && PES == 2) {
+      // one exponent per (head, 256-channel half): the max over both owners
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < HT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a = fmaxf(a, fabsf(o[i][j]));
+      a = rows_max(a);
+      if (g == 0) lds_ml[wave][0][c16] = a;          // lds_ml was last read before the barrier above
+      __syncthreads();
+      a = fmaxf(a, lds_ml[pw][0][c16]);
+      if (a > 0.f && a <= 3.0e38f) { (void)frexpf(a, &e2); e2 = 15 - e2; }   // a < 2^(15 - e2)
+    }
+    __syncthreads();   // every passed half read before the staging reuses the buffers
+    uint8_t* sb0 = reinterpret_cast<uint8_t*>(lds_ring);
+    if (!split) {
+      constexpr int kRowB = HT * 16 * 2 + 32;
+      constexpr int kCph = HT * 16 * 2 / 16;
+      uint8_t* sb = sb0 + (size_t)wave * 16 * kRowB;
+      const float inv = k.padded ? 0.f : 1.f / L;
+#pragma unroll
+      for (int i = 0; i < HT; ++i)
+        *reinterpret_cast<uint2*>(sb + c16 * kRowB + (i * 16 + g * 4) * 2) =
+            make_uint2(pack2<QT>(o[i][0] * inv, o[i][1] * inv),
+                       pack2<QT>(o[i][2] * inv, o[i][3] * inv));
+      uint8_t* ob = p.out + (((size_t)t * p.H + h0) * kDV + chw) * 2;
+      store_rows<kCph, kRowB, kDV * 2>(sb, ob, p.out_nt, lane);
+      if (g == 0 && cs == 0 && kw == 0) p.lse[(size_t)t * p.H + hq] = k.padded ? 0.f : M * kLn2 + logf(L);
+    } else {
+      constexpr int kRowB = HT * 16 * PES + (PES == 2 ? 32 : 16);
+      constexpr int kCph = HT * 16 * PES / 16;
+      uint8_t* sb = sb0 + (size_t)wave * 16 * kRowB;
+      if constexpr (PES == 2) {
+#pragma unroll
+        for (int i = 0; i < HT; ++i)
+          *reinterpret_cast<uint2*>(sb + c16 * kRowB + (i * 16 + g * 4) * 2) =
+              make_uint2(pack2<_Float16>(ldexpf(o[i][0], e2), ldexpf(o[i][1], e2)),
+                         pack2<_Float16>(ldexpf(o[i][2], e2), ldexpf(o[i][3], e2)));
+      } else {
+#pragma unroll
+        for (int i = 0; i < HT; ++i)
+          *reinterpret_cast<f32x4*>(sb + c16 * kRowB + (i * 16 + g * 4) * 4) = o[i];
+      }
+      const size_t row0 = ((size_t)t * p.nsplit + k.sp) * p.H + h0;
+      uint8_t* ob = p.part_o + (row0 * kDV + chw) * PES;
+      store_rows<kCph, kRowB, kDV * PES>(sb, ob, p.part_nt, lane);
+      if (g == 0 && kw == 0) {
+        float* pm = p.part_ml + (row0 + c16) * 4;   // (m, l, e_lo, e_hi); l < 0 marks a padded token
+        if (cs == 0) *reinterpret_cast<float2*>(pm) = make_float2(M, k.padded ? -1.f : L);
+        pm[2 + cs] = (float)e2;
+      }
+    }
+    return;
+  }
+#endif
   if constexpr (KW > 1) {
     if (g == 0) { lds_ml[wave][0][c16] = m_run; lds_ml[wave][1][c16] = l_run; }
     __syncthreads();
