@@ -28,6 +28,7 @@
 // 16x16x16 MFMAs per 16-channel tile.
 
 #include <type_traits>
+#include <utility>
 
 #include "sas_kern.h"
 
@@ -51,6 +52,25 @@ struct BwdParams {
   float* d_cmp;         // [cmp rows, D] fp32, accumulated (null for SWA)
   float* d_sinks;       // [H] fp32, accumulated
 };
+
+// f(integral_constant<int, j>) for j = 0 .. N-1, with no loop: arrays
+// indexed this way are split into registers, while an array indexed inside a
+// loop (even one unrolled later) is first moved to LDS or scratch memory by
+// the compiler, which made each row-chunk prefetch a load waited for at once.
+template <typename F, int... I>
+__device__ __forceinline__ void unroll_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void unroll(F&& f) {
+  unroll_impl(f, std::make_integer_sequence<int, N>{});
+}
+// 16 bytes of a cache row by a global (not flat) load: vmcnt only, so the
+// wait for it leaves the LDS counter alone
+__device__ __forceinline__ uint4 load_row16(uint64_t addr) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(uint4, *reinterpret_cast<const __attribute__((address_space(1))) u32x4*>(addr));
+}
 
 template <typename QT>
 __device__ __forceinline__ float to_f(uint16_t v) {
@@ -176,28 +196,27 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
   uint4 rbuf[NLD];
   auto load_rows = [&](int c0n) {
     const int nrn = min(kBwdRows, k.nvalid - c0n);
-#pragma unroll
-    for (int j = 0; j < NLD; ++j) {
+    unroll<NLD>([&](auto J) {
+      constexpr int j = decltype(J)::value;
       const int i = tid + NT * j;
       if (i < kBwdRows * CH) {
         const int r = i / CH, c = i - r * CH;
-        const uint64_t a = lds_rows[c0n + min(r, nrn - 1)];
-        rbuf[j] = *reinterpret_cast<const uint4*>(a + c * 16);
+        rbuf[j] = load_row16(lds_rows[c0n + min(r, nrn - 1)] + c * 16);
       }
-    }
+    });
   };
   if (k.nvalid > 0) load_rows(0);
 
   for (int c0 = 0; c0 < k.nvalid; c0 += kBwdRows) {
     const int nr = min(kBwdRows, k.nvalid - c0);
-#pragma unroll
-    for (int j = 0; j < NLD; ++j) {
+    unroll<NLD>([&](auto J) {
+      constexpr int j = decltype(J)::value;
       const int i = tid + NT * j;
       if (i < kBwdRows * CH) {
         const int r = i / CH, c = i - r * CH;
         *reinterpret_cast<uint4*>(lds_k + r * KS + c * 16) = rbuf[j];
       }
-    }
+    });
     __syncthreads();
     if (c0 + kBwdRows < k.nvalid) load_rows(c0 + kBwdRows);
     // S^T[key][head] = K . Q^T and dP^T = V . dO^T by 16x16x32 MFMA, the
@@ -414,27 +433,27 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
   uint4 rbuf[NLD];
   auto load_rows = [&](int c0n) {
     const int nrn = min(kBwdRows, k.nvalid - c0n);
-#pragma unroll
-    for (int j = 0; j < NLD; ++j) {
+    unroll<NLD>([&](auto J) {
+      constexpr int j = decltype(J)::value;
       const int i = tid + NT * j;
       if (i < kBwdRows * CH) {
         const int r = i / CH, c = i - r * CH;
-        rbuf[j] = *reinterpret_cast<const uint4*>(lds_rows[c0n + min(r, nrn - 1)] + c * 16);
+        rbuf[j] = load_row16(lds_rows[c0n + min(r, nrn - 1)] + c * 16);
       }
-    }
+    });
   };
   if (k.nvalid > 0) load_rows(0);
 
   for (int c0 = 0; c0 < k.nvalid; c0 += kBwdRows) {
     const int nr = min(kBwdRows, k.nvalid - c0);
-#pragma unroll
-    for (int j = 0; j < NLD; ++j) {
+    unroll<NLD>([&](auto J) {
+      constexpr int j = decltype(J)::value;
       const int i = tid + NT * j;
       if (i < kBwdRows * CH) {
         const int r = i / CH, c = i - r * CH;
         *reinterpret_cast<uint4*>(lds_k + r * KS + c * 16) = rbuf[j];
       }
-    }
+    });
     __syncthreads();   // the chunk (and, the first time, dO) in LDS
     if (c0 + kBwdRows < k.nvalid) load_rows(c0 + kBwdRows);
     // this wave's channel half of S^T = K . Q^T and dP^T = V . dO^T for its
