@@ -65,13 +65,6 @@ template <int N, typename F>
 __device__ __forceinline__ void unroll(F&& f) {
   unroll_impl(f, std::make_integer_sequence<int, N>{});
 }
-// 16 bytes of a cache row by a global (not flat) load: vmcnt only, so the
-// wait for it leaves the LDS counter alone
-__device__ __forceinline__ uint4 load_row16(uint64_t addr) {
-  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-  return __builtin_bit_cast(uint4, *reinterpret_cast<const __attribute__((address_space(1))) u32x4*>(addr));
-}
-
 template <typename QT>
 __device__ __forceinline__ float to_f(uint16_t v) {
   return (float)__builtin_bit_cast(QT, v);
@@ -201,7 +194,7 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
       const int i = tid + NT * j;
       if (i < kBwdRows * CH) {
         const int r = i / CH, c = i - r * CH;
-        rbuf[j] = load_row16(lds_rows[c0n + min(r, nrn - 1)] + c * 16);
+        rbuf[j] = gld16(lds_rows[c0n + min(r, nrn - 1)] + c * 16);
       }
     });
   };
@@ -438,7 +431,7 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
       const int i = tid + NT * j;
       if (i < kBwdRows * CH) {
         const int r = i / CH, c = i - r * CH;
-        rbuf[j] = load_row16(lds_rows[c0n + min(r, nrn - 1)] + c * 16);
+        rbuf[j] = gld16(lds_rows[c0n + min(r, nrn - 1)] + c * 16);
       }
     });
   };

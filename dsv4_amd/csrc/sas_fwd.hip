@@ -215,12 +215,12 @@ struct Fwd {
       fbuf[k] = make_uint4(0, 0, 0, 0);
       fsc[k] = 0.f;
       if (e < C::TR * C::FCPR && r < nk) {
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(lds_rows[rp + r]);
+        const uint64_t src = lds_rows[rp + r];
         if (c < 32) {
-          fbuf[k] = *reinterpret_cast<const uint4*>(src + c * 16);
-          fsc[k] = *reinterpret_cast<const float*>(src + 512 + 4 * (c >> 3));
+          fbuf[k] = gld16(src + c * 16);
+          fsc[k] = gldf(src + 512 + 4 * (c >> 3));
         } else {
-          fbuf[k] = *reinterpret_cast<const uint4*>(src + 528 + (c - 32) * 16);
+          fbuf[k] = gld16(src + 528 + (c - 32) * 16);
         }
       }
     }
@@ -1215,17 +1215,17 @@ struct Dec {
     const int i = step * 16 + c16;
     const bool live = step < nsteps;
     const uint64_t ra = lds_rows[rbeg + min(i, max(nrows - 1, 0))];
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(live && i < nrows ? ra : dummy);
+    const uint64_t src = live && i < nrows ? ra : dummy;
     const int gm = live ? g : 0, lm = live ? 1 : 0;
     if constexpr (!KVF) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) st.k[ks] = *reinterpret_cast<const uint4*>(src + lm * (4 * ks + gm) * 16);
+      for (int ks = 0; ks < KS; ++ks) st.k[ks] = gld16(src + lm * (4 * ks + gm) * 16);
     } else {
 #pragma unroll
-      for (int ks = 0; ks < 16; ++ks) st.l8[ks] = *reinterpret_cast<const uint2*>(src + lm * (4 * ks + gm) * 8);
-      st.sc = *reinterpret_cast<const float4*>(src + lm * 512);
-      st.k[0] = *reinterpret_cast<const uint4*>(src + lm * (528 + gm * 16));
-      st.k[1] = *reinterpret_cast<const uint4*>(src + lm * (528 + (4 + gm) * 16));
+      for (int ks = 0; ks < 16; ++ks) st.l8[ks] = gld8(src + lm * (4 * ks + gm) * 8);
+      st.sc = gld16f(src + lm * 512);
+      st.k[0] = gld16(src + lm * (528 + gm * 16));
+      st.k[1] = gld16(src + lm * (528 + (4 + gm) * 16));
     }
   }
 

@@ -59,6 +59,25 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
+// Loads of cache rows whose addresses are held as integers (the compacted
+// row lists): through global-address-space pointers, so they compile to
+// global loads, counted by vmcnt only. Through generic pointers they become
+// flat loads, which count against lgkmcnt as well, so every LDS wait issued
+// while they are in flight waits for them too.
+#define SAS_GLOBAL __attribute__((address_space(1)))
+typedef unsigned u32x4g __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2g __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 gld16(uint64_t a) {
+  return __builtin_bit_cast(uint4, *reinterpret_cast<const SAS_GLOBAL u32x4g*>(a));
+}
+__device__ __forceinline__ uint2 gld8(uint64_t a) {
+  return __builtin_bit_cast(uint2, *reinterpret_cast<const SAS_GLOBAL u32x2g*>(a));
+}
+__device__ __forceinline__ float gldf(uint64_t a) { return *reinterpret_cast<const SAS_GLOBAL float*>(a); }
+__device__ __forceinline__ float4 gld16f(uint64_t a) {
+  return __builtin_bit_cast(float4, *reinterpret_cast<const SAS_GLOBAL u32x4g*>(a));
+}
+
 static __shared__ __attribute__((aligned(16))) uint4 lds_ring[kLdsRows * kChunksMax];  // 147,456 B
 // compacted rows of the workgroup: the byte address of each cache row
 static __shared__ uint64_t lds_rows[kMaxSlots];
