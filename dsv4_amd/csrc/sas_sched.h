@@ -50,6 +50,9 @@ template <typename T> SAS_HD inline T smin(T a, T b) { return b < a ? b : a; }
 
 template <typename W>
 SAS_HD inline W floordiv(W a, W b) {
+  // non-negative operands below 2^32 (nearly every use): a 32-bit division,
+  // the same quotient (the device has no 64-bit divider)
+  if (a >= 0 && b > 0 && a <= (W)0xffffffffu && b <= (W)0xffffffffu) return (W)((uint32_t)a / (uint32_t)b);
   W q = a / b;
   if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
   return q;
@@ -236,16 +239,41 @@ struct RowInfo {
   i64 cost, blocks, last_cost, s2_start;
 };
 
+// The row phase of a core's fill (metadata.py:750-764): rows of the current
+// unit, from the current one (c), each taken while it fits its limit plus
+// half its last block's cost; rows without blocks are stepped over. Returns
+// false when one step runs over more than max_skip rows without blocks.
+template <typename W, typename RowFn>
+SAS_HD bool scan_rows(RowFn& row_info, i64 cur_b, const BatchCtx<W>& bc, i64 limit, i64 max_skip, i64& cur_row,
+                      RowInfo& c, i64& cur_s2, i64& ccost, i64& cblock, i64& bn2_cost, i64& bn2_block) {
+  while (limit + c.last_cost / 2 >= ccost + c.cost) {
+    ccost += c.cost;
+    cblock += c.blocks;
+    bn2_cost = smax<i64>(0, bn2_cost - c.cost);
+    bn2_block = smax<i64>(0, bn2_block - c.blocks);
+    i64 guard = 0;
+    do {
+      cur_row += 1;
+      c = row_info(cur_b, bc, cur_row);
+      if (++guard > max_skip) return false;
+    } while (c.blocks == 0);
+    cur_s2 = c.s2_start;
+  }
+  return true;
+}
+
 // Greedy assignment of the cores (metadata.py:718-764, 872-923, 959-964).
 // `bat` gives, per batch b, its row count / tail and summed cost / blocks /
 // last block cost: bat.num(b), bat.tail(b), bat.cost(b), bat.block(b),
-// bat.last(b); `row_info(b, bc, row)` one row's figures. Core i's end
-// (bn2, m, s2) goes to ends[i] for i < cap (zeroed by the caller). Returns
-// the number of cores used, or -1 when a row scan steps over more than
-// max_skip rows without blocks.
-template <typename W, typename Bat, typename RowFn>
+// bat.last(b); `row_info(b, bc, row)` one row's figures; `scan(cur_b, bc,
+// limit, cur_row, c, cur_s2, ccost, cblock, bn2_cost, bn2_block)` the row
+// phase, scan_rows's contract (the device runs it with the whole workgroup).
+// Core i's end (bn2, m, s2) goes to ends[i] for i < cap (zeroed by the
+// caller). Returns the number of cores used, or -1 when a row scan steps
+// over more than max_skip rows without blocks.
+template <typename W, typename Bat, typename RowFn, typename ScanFn>
 SAS_HD i64 assign(const Sched<W>& s, const Bat& bat, i64 total_cost, i64 max_row_cost, bool all_zero,
-                  RowFn&& row_info, i64 (*ends)[3], i64 cap, i64 max_skip) {
+                  RowFn&& row_info, i64 (*ends)[3], i64 cap, ScanFn&& scan) {
   const i64 aic = s.in.aic, B = s.B, hkv = s.in.heads_kv;
   if (all_zero) {
     if (cap > 0) { ends[0][0] = B * hkv; ends[0][1] = 0; ends[0][2] = 0; }
@@ -281,21 +309,7 @@ SAS_HD i64 assign(const Sched<W>& s, const Bat& bat, i64 total_cost, i64 max_row
         cur_s2 = c.s2_start;
       }
       // single rows
-      if (!finished) {
-        while (limit + c.last_cost / 2 >= ccost + c.cost) {
-          ccost += c.cost;
-          cblock += c.blocks;
-          bn2_cost = smax<i64>(0, bn2_cost - c.cost);
-          bn2_block = smax<i64>(0, bn2_block - c.blocks);
-          i64 guard = 0;
-          do {
-            cur_row += 1;
-            c = row_info(cur_b, bc, cur_row);
-            if (++guard > max_skip) return -1;
-          } while (c.blocks == 0);
-          cur_s2 = c.s2_start;
-        }
-      }
+      if (!finished && !scan(cur_b, bc, limit, cur_row, c, cur_s2, ccost, cblock, bn2_cost, bn2_block)) return -1;
       if (i < cap) { ends[i][0] = cur_bn2; ends[i][1] = cur_row; ends[i][2] = cur_s2; }
       unassigned -= ccost;
     }
@@ -372,7 +386,11 @@ i64 run_host(const Inputs& in, bool saturate, i64 max_skip, int32_t* out, int me
   };
   std::vector<i64> ends(3 * (size_t)smax<i64>(in.aic, 1), 0);
   auto* e3 = reinterpret_cast<i64(*)[3]>(ends.data());
-  const i64 used = assign(s, bat, total_cost, max_row_cost, all_zero, row_info, e3, in.aic, max_skip);
+  auto scan = [&](i64 b, const BatchCtx<W>& bc, i64 limit, i64& cur_row, RowInfo& c, i64& cur_s2, i64& ccost,
+                  i64& cblock, i64& bn2_cost, i64& bn2_block) {
+    return scan_rows<W>(row_info, b, bc, limit, max_skip, cur_row, c, cur_s2, ccost, cblock, bn2_cost, bn2_block);
+  };
+  const i64 used = assign(s, bat, total_cost, max_row_cost, all_zero, row_info, e3, in.aic, scan);
   if (used < 0) return -1;
   write_rows(in.aic, used, e3, out, meta_size, aic_rows, row_size);
   return used;

@@ -53,9 +53,10 @@ def test_device_scheduler_matches_host_fuzz():
 
 @pytest.mark.parametrize("name", ["C2", "C3", "scfa_prefill"])
 def test_device_scheduler_at_benchmark_shapes(name):
-    """The decode and prefill workloads (C3: 4096 query rows; the
-    reference's 8K prefill: rows past the 6144 kept in LDS are computed by
-    the assigning thread): same rows as the host, and the launch time."""
+    """The decode and prefill workloads (C3: 4096 query rows, the row phase
+    over windows of rows; the reference's 8K prefill: rows past the 5120
+    kept in LDS are computed on the spot): same rows as the host, and the
+    time a call takes."""
     cfg = C.CONFIGS.get(name) or C.REF_SCENARIOS[name]
     ql, kl = C.seq_lengths(cfg)
     cu = [0]
