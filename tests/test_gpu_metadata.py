@@ -51,6 +51,44 @@ def test_device_scheduler_matches_host_fuzz():
     assert n_dev > 300   # most cases pass lengths, so they ran on the device
 
 
+def _long_unit_kwargs(rnd):
+    """Few batches of hundreds to thousands of query rows over few cores: the
+    row phase scans many windows of rows within one unit, with runs of rows
+    without blocks (short or empty KV, sliding windows that end early)."""
+    B = rnd.choice([1, 2, 3])
+    n2 = rnd.choice([1, 2])
+    g = rnd.choice([1, 16, 64])
+    ql = [rnd.choice([300, 1000, 3000]) for _ in range(B)]
+    kl = [max(0, q + rnd.choice([-2900, -700, -1, 0, 1, 511, 4000])) for q in ql]
+    cu = [0]
+    for x in ql:
+        cu.append(cu[-1] + x)
+    kw = dict(num_heads_q=g * n2, num_heads_kv=n2, head_dim=576, batch_size=B, max_seqlen_q=max(ql),
+              max_seqlen_kv=max(kl), layout_q="TND", cu_seqlens_q=torch.tensor(cu, dtype=torch.int32),
+              seqused_kv=torch.tensor(kl, dtype=torch.int32), has_cmp_kv=rnd.random() < 0.7,
+              aic_core_num=rnd.choice([1, 2, 3, 5, 24]), ori_win_left=rnd.choice([127, 0, 511, -1]),
+              ori_mask_mode=rnd.choice([4, 4, 3, 0]))
+    if kw["has_cmp_kv"]:
+        kw["cmp_ratio"] = rnd.choice([1, 4, 128])
+        kw["cmp_topk"] = rnd.choice([0, 64, 512])
+    return kw
+
+
+def test_device_scheduler_long_row_scans_match_host():
+    rnd = random.Random(20262)
+    for i in range(60):
+        kw = _long_unit_kwargs(rnd)
+        try:
+            host = sparse_attn_sharedkv_metadata(**kw).tolist()
+        except ValueError:
+            host = None
+        dev = sparse_attn_sharedkv_metadata(**_on_device(kw)).cpu().tolist()
+        if host is None:
+            assert dev[0] == -1, f"case {i}: {kw}"
+        else:
+            assert dev == host, f"case {i}: {kw}"
+
+
 @pytest.mark.parametrize("name", ["C2", "C3", "scfa_prefill"])
 def test_device_scheduler_at_benchmark_shapes(name):
     """The decode and prefill workloads (C3: 4096 query rows, the row phase
