@@ -69,7 +69,7 @@ struct Cfg {
   // a pair sums S over its half of the D channels and the pair adds the two
   // halves through LDS (no QK^T work is duplicated). The exchange buffer
   // takes the ring rows above kRingRows.
-  static constexpr bool QS = CS == 2 && !KVF;
+  static constexpr bool QS = CS == 2;
   static constexpr int kRingRows = QS ? 96 : kLdsRows;
   // rows per step: 32, or 16 when 32-row slots would leave a ring shallower than 2
   static constexpr int TR = kRingRows / (KW * 32) < 2 ? 16 : 32;
@@ -96,7 +96,12 @@ struct Cfg {
   static constexpr int SLOT = TR * kChunksMax;              // slot stride (chunks)
   static constexpr int CH = D / 8;                          // 16-byte chunks per bf16 row
   static constexpr int KS = D / 32;                         // QK^T k-steps
-  static constexpr int KSQ = QS ? KS / 2 : KS;              // k-steps of one wave
+  // k-steps of one wave. fp8 rows: S is summed per 128-channel scale group
+  // (4 k-steps) and each group's sum scaled in fp32, so a channel split
+  // follows the groups: half 0 takes groups 0-1 and the two rope k-steps,
+  // half 1 groups 2-3 and two k-steps of zero Q (10 each).
+  static constexpr int KSQ = QS ? (KVF ? 10 : KS / 2) : KS;
+  static constexpr int NLG = QS ? 2 : 4;                    // fp8: scale groups per wave
   static constexpr int GT = WK * 64;                        // threads per key-group
   static constexpr int NI = TR * CH / 64;                   // DMA instructions per step
   static constexpr int OPS = (NI + WK - 1) / WK;            // most DMA ops per wave per step
@@ -105,6 +110,7 @@ struct Cfg {
   static constexpr int FCPR = 40;
   static constexpr int FOPS = (TR * FCPR + GT - 1) / GT;
   static_assert(TR * CH % 64 == 0, "whole DMA instructions");
+  static_assert(!KVF || (KS == 18 && CH == kChunksMax), "fp8 rows: 512 latent + 64 rope channels");
   static_assert(NST >= 2 && NST <= 4, "ring depth");
   static_assert((NST - 1) * OPS < 64, "vmcnt range");
   static_assert(KW * NST * SLOT <= kRingRows * kChunksMax, "ring fits");
@@ -138,6 +144,11 @@ struct Fwd {
         nops((C::NI - wave % C::WK + C::WK - 1) / C::WK) {}
 
   __device__ __forceinline__ int slot(int j) const { return ring + j * C::SLOT; }
+  // QK^T k-steps: this wave's first one, and the one its local k-step ks
+  // computes (fp8 channel halves: local k-steps 8 and 9 are the rope k-steps
+  // 16 and 17, with zero Q in half 1)
+  __device__ __forceinline__ int kbase() const { return C::QS ? (KVF ? cs * 8 : cs * C::KSQ) : 0; }
+  __device__ __forceinline__ int kglob(int ks) const { return (KVF && C::QS && ks >= 8) ? ks + 8 : kbase() + ks; }
 
   // -- bf16 / fp16 rows: DMA one step into slot j ------------------------------
   // Lane `lane` of the wave's o-th instruction of a step moves row drow(o) of
@@ -198,8 +209,9 @@ struct Fwd {
       const uint4* qr = &lds_ring[C::kQRow0 * kChunksMax + h * C::CH];
 #pragma unroll
       for (int ks = 0; ks < C::KSQ; ++ks) {
-        const int L = 4 * (cs * C::KSQ + ks) + g;
+        const int L = 4 * kglob(ks) + g;
         qf[n][ks] = qr[(L & -SG) | ((L & (SG - 1)) ^ hsw)];
+        if (KVF && C::QS && ks >= 8 && cs == 1) qf[n][ks] = make_uint4(0, 0, 0, 0);
       }
     }
   }
@@ -235,12 +247,15 @@ struct Fwd {
       uint4* row = &lds_ring[sl + r * C::CH];
       const int sw = swz<C::CH>(r);
       if (c < 32) {
+        // the e4m3 values unscaled (exact in bf16); the group's scale goes to
+        // the scale table, applied to S and P in fp32 (qk, pv)
         const uint32_t w[4] = {fbuf[k].x, fbuf[k].y, fbuf[k].z, fbuf[k].w};
         uint32_t o[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e4m3x4_to_bf16(w[i], fsc[k], o[2 * i], o[2 * i + 1]);
+        for (int i = 0; i < 4; ++i) e4m3x4_to_bf16(w[i], 1.f, o[2 * i], o[2 * i + 1]);
         row[(2 * c) ^ sw] = make_uint4(o[0], o[1], o[2], o[3]);
         row[(2 * c + 1) ^ sw] = make_uint4(o[4], o[5], o[6], o[7]);
+        if ((c & 7) == 0) lds_fsc[c >> 3][sl / C::CH + r] = fsc[k];
       } else {
         row[(64 + c - 32) ^ sw] = fbuf[k];
       }
@@ -275,12 +290,27 @@ struct Fwd {
     int qo[KPG];
 #pragma unroll
     for (int j = 0; j < KPG; ++j) {
-      const int L = 4 * ((C::QS ? cs * C::KSQ : 0) + j) + g;
+      const int L = 4 * (kbase() + j) + g;
       qo[j] = (L & -SG) | ((L & (SG - 1)) ^ ksw);
     }
     auto kfrag = [&](int ks, int mt) {
-      return qrow[mt * 16 * C::CH + (ks / KPG) * SG + qo[ks % KPG]];
+      return qrow[mt * 16 * C::CH + (ks / KPG) * SG + qo[ks % KPG] + (kglob(ks) - kbase() - ks) * 4];
     };
+    // fp8 rows: S = sum over the wave's scale groups of scale (per row, fp32)
+    // x that group's MFMA chain (unscaled e4m3 values, exact), plus the rope
+    // k-steps, which accumulate straight into sacc. Two group chains
+    // alternate so one is folded while the next runs. fs: the scales of the
+    // lane's four rows 4g..4g+3 of each row tile.
+    constexpr int NG8 = KVF ? C::NLG : 1, SRT = C::Q2 ? 1 : MT;
+    f32x4 gacc[2][MT], fs[NG8][SRT];
+    if constexpr (KVF) {
+      const int rr = sl / C::CH + (C::Q2 ? (hw & 1) * 16 : 0) + 4 * g;
+      const int g0 = C::QS ? 2 * cs : 0;
+#pragma unroll
+      for (int lg = 0; lg < NG8; ++lg)
+#pragma unroll
+        for (int t = 0; t < SRT; ++t) fs[lg][t] = *reinterpret_cast<const f32x4*>(&lds_fsc[g0 + lg][rr + t * 16]);
+    }
     constexpr int kPfK = C::PFK;
     constexpr int RT = C::Q2 ? 1 : MT;   // K row tiles read per k-step
     uint4 af[kPfK][RT];
@@ -302,8 +332,24 @@ struct Fwd {
       for (int mt = 0; mt < MT; ++mt) {
         const uint4 am = a[C::Q2 ? 0 : mt];
         const uint4 bq = qf[C::Q2 ? mt : 0][ks];
-        if (C::CH2 && (ks & 1)) sodd[mt] = mfma32k<QT>(am, bq, sodd[mt]);
-        else sacc[mt] = mfma32k<QT>(am, bq, sacc[mt]);
+        if constexpr (KVF) {
+          if (ks < 4 * C::NLG) {
+            f32x4& ga = gacc[(ks / 4) & 1][mt];
+            ga = mfma32k<QT>(am, bq, ks % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : ga);
+          } else {
+            sacc[mt] = mfma32k<QT>(am, bq, sacc[mt]);
+          }
+        } else if (C::CH2 && (ks & 1)) {
+          sodd[mt] = mfma32k<QT>(am, bq, sodd[mt]);
+        } else {
+          sacc[mt] = mfma32k<QT>(am, bq, sacc[mt]);
+        }
+      }
+      if constexpr (KVF) {
+        if (ks < 4 * C::NLG && ks % 4 == 3) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) sacc[mt] += fs[ks / 4][C::Q2 ? 0 : mt] * gacc[(ks / 4) & 1][mt];
+        }
       }
       if ((ks & 1) && ks / 2 < C::OPS) dma(ks / 2);
       if constexpr (kMid) mid(ks);
@@ -311,10 +357,11 @@ struct Fwd {
     // schedule: the prefetch reads first, then per k-step MT MFMAs + RT reads
     // (+ a share of the other step's VALU work). Placed before the remaining
     // DMA issues: a wave-dependent guard there starts a new basic block, and
-    // these groups order only the instructions of their own block.
-    __builtin_amdgcn_sched_group_barrier(0x100, RT * kPfK, 0);
+    // these groups order only the instructions of their own block. (fp8
+    // rows: the compiler's own order around the scale reads and folds.)
+    if constexpr (!KVF) __builtin_amdgcn_sched_group_barrier(0x100, RT * kPfK, 0);
 #pragma unroll
-    for (int ks = 0; ks < C::KSQ; ++ks) {
+    for (int ks = 0; ks < (KVF ? 0 : C::KSQ); ++ks) {
       __builtin_amdgcn_sched_group_barrier(0x008, MT, 0);
       if (ks + kPfK < C::KSQ) __builtin_amdgcn_sched_group_barrier(0x100, RT, 0);
       if constexpr (kMid) __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
@@ -445,6 +492,28 @@ struct Fwd {
 #pragma unroll
     for (int q = 0; q < TPG; ++q) voff[q] = ((2 * q + vb) ^ vsw) * 16;
     constexpr int kPfV = C::PFV;
+    // fp8 rows: V holds the unscaled e4m3 values, so channel tile mt of scale
+    // group G takes the B operand P x scale[G] (P as rounded to the query
+    // dtype, times the key's fp32 scale, rounded once more); the lane's keys
+    // are rows 4g..4g+3 (+16) of the step, as in S^T.
+    constexpr int NG8 = KVF ? C::NLG : 1, TPL = C::NTL / NG8;   // channel tiles per group
+    uint32_t pks[NG8][2 * MT];
+    if constexpr (KVF) {
+      const int rr = sl / C::CH + 4 * g;
+      const int g0 = C::QS ? 2 * cs : 0;
+#pragma unroll
+      for (int lg = 0; lg < NG8; ++lg)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const f32x4 f = *reinterpret_cast<const f32x4*>(&lds_fsc[g0 + lg][rr + mt * 16]);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t w = pk[mt * 2 + h];
+            pks[lg][mt * 2 + h] = pack2<QT>(__uint_as_float(w << 16) * f[2 * h],
+                                            __uint_as_float(w & 0xffff0000u) * f[2 * h + 1]);
+          }
+        }
+    }
     if constexpr (MT == 2) {
       auto vfrag = [&](int mt) {
         const char* a0 = vbase + (mt / TPG) * TPG * 32 + voff[mt % TPG];
@@ -461,7 +530,8 @@ struct Fwd {
       for (int mt = 0; mt < C::NTL; ++mt) {
         const uint4 a = vf[mt % kPfV];
         if (mt + kPfV < C::NTL) vf[mt % kPfV] = vfrag(mt + kPfV);
-        acc[mt] = mfma32k<QT>(a, pfrag, acc[mt]);
+        const int lg = mt / TPL;
+        acc[mt] = mfma32k<QT>(a, KVF ? make_uint4(pks[lg][0], pks[lg][1], pks[lg][2], pks[lg][3]) : pfrag, acc[mt]);
         if (mt % 3 == 2 && mt / 3 < C::OPS) dma(mt / 3);
       }
 #pragma unroll
@@ -488,7 +558,8 @@ struct Fwd {
       for (int mt = 0; mt < C::NTL; ++mt) {
         const uint2 a = vf[mt % kPf];
         if (mt + kPf < C::NTL) vf[mt % kPf] = vfrag(mt + kPf);
-        acc[mt] = mfma16k<QT>(a, pfrag, acc[mt]);
+        const int lg = mt / TPL;
+        acc[mt] = mfma16k<QT>(a, KVF ? make_uint2(pks[lg][0], pks[lg][1]) : pfrag, acc[mt]);
       }
       __builtin_amdgcn_sched_group_barrier(0x100, kPf, 1);
 #pragma unroll
@@ -572,9 +643,10 @@ struct Fwd {
         compute(slot(J), it, [&](int o) { if (more) fire(d, o); });
       }
     } else {
-      // fp8: registers hold step it+1; slot J holds step it
+      // fp8: registers hold step it+1; slot J holds step it (with QS every
+      // wave takes the S exchange barrier of every step)
       step_sync();
-      if (it < nsteps) compute(slot(J), it, [](int) {});
+      if (it < nsteps || C::QS) compute(slot(J), it, [](int) {});
       if (it + 1 < nsteps) fstore((J + 1) % C::NST);
       if (it + 2 < nsteps) fload(it + 2);
     }
@@ -1175,7 +1247,7 @@ sas_fwd_kernel(const FwdParams p) {
 // wave are in flight with no LDS staging; the QK^T MFMAs read those
 // registers. Only the V half (channels 0..511) passes through LDS, written
 // from the same registers into a per-wave tile that the PV operand reads
-// transposed. fp8 rows are dequantised in registers on the way.
+// transposed. (fp8 rows take the LDS kernels.)
 
 template <int D, typename QT, int KVF>
 struct Dec {
@@ -1186,14 +1258,14 @@ struct Dec {
   // 16-chunk-group one costs the kernel its registers)
   static constexpr int VRS = VCH + 8;
   static constexpr int VT = 16 * VRS;        // chunks per V tile
-  static constexpr int ROWB = KVF ? kRow656 : D * 2;
-  static_assert(!KVF || D == 576, "fp8 rows carry 576 channels");
+  static constexpr int ROWB = D * 2;
+  // fp8 rows take the LDS kernels, which apply the scales per 128-channel
+  // group to S and P in fp32
+  static_assert(!KVF, "cache rows in the query dtype only");
   static_assert(4 * VT <= kLdsRows * kChunksMax, "V tiles fit");
 
   struct Stage {
-    uint4 k[KVF ? 2 : KS];    // bf16 chunks (fp8: the two rope chunks)
-    uint2 l8[KVF ? 16 : 1];   // fp8: 8 latent bytes per k-step
-    float4 sc;                // fp8: the row's 4 scales
+    uint4 k[KS];   // the row's chunks 4ks + g
   };
 
   const FwdParams& p;
@@ -1217,31 +1289,12 @@ struct Dec {
     const uint64_t ra = lds_rows[rbeg + min(i, max(nrows - 1, 0))];
     const uint64_t src = live && i < nrows ? ra : dummy;
     const int gm = live ? g : 0, lm = live ? 1 : 0;
-    if constexpr (!KVF) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) st.k[ks] = gld16(src + lm * (4 * ks + gm) * 16);
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < 16; ++ks) st.l8[ks] = gld8(src + lm * (4 * ks + gm) * 8);
-      st.sc = gld16f(src + lm * 512);
-      st.k[0] = gld16(src + lm * (528 + gm * 16));
-      st.k[1] = gld16(src + lm * (528 + (4 + gm) * 16));
-    }
+    for (int ks = 0; ks < KS; ++ks) st.k[ks] = gld16(src + lm * (4 * ks + gm) * 16);
   }
 
-  // bf16 A-operand chunk 4ks + g of the lane's row
-  __device__ __forceinline__ uint4 kchunk(const Stage& st, int ks) const {
-    if constexpr (!KVF) {
-      return st.k[ks];
-    } else {
-      if (ks >= 16) return st.k[ks - 16];
-      const float sc = ks < 4 ? st.sc.x : ks < 8 ? st.sc.y : ks < 12 ? st.sc.z : st.sc.w;
-      uint32_t o[4];
-      e4m3x4_to_bf16(st.l8[ks].x, sc, o[0], o[1]);
-      e4m3x4_to_bf16(st.l8[ks].y, sc, o[2], o[3]);
-      return make_uint4(o[0], o[1], o[2], o[3]);
-    }
-  }
+  // A-operand chunk 4ks + g of the lane's row
+  __device__ __forceinline__ uint4 kchunk(const Stage& st, int ks) const { return st.k[ks]; }
 
   template <int J, bool REFILL>
   __device__ __forceinline__ void step(Stage (&st)[NP], int it0) {
@@ -1456,10 +1509,11 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
     // merge (32-token, 64-head decode: 18.4 µs at 32 heads x 4 splits,
     // 21.1 µs at 64 heads x 8 splits); else 64-head groups, which leave room
     // for twice the splits (31-token, 128-head decode: 28.7 µs at 64 x 4
-    // against 32.4 µs at 32 x 2). fp8 rows take 64-head groups (4 waves
-    // only; 8-token, 128-head fp8 decode: 25.6 µs against 31.7 µs).
+    // against 32.4 µs at 32 x 2). fp8 rows alike (8-token, 128-head fp8
+    // decode: 23.2 µs at 32 heads x 8 waves x 8 splits, 26.3 µs at 64 heads
+    // x 4 waves x 12 splits).
     if (a->H % 64 == 0 && T * (a->H / 64) >= 2 * cus) hw = 4;
-    else if (a->H % 64 == 0 && (fp8 || one_round_splits(2) < 4)) hw = 4;
+    else if (a->H % 64 == 0 && one_round_splits(2) < 4) hw = 4;
     else if (a->H % 32 == 0) hw = 2;
     else hw = 1;
   }
@@ -1469,9 +1523,9 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   // 8 waves: two per SIMD, a pair per 16 heads splitting both the QK^T and
   // the O channels; the second wave on a SIMD overlaps the other's LDS and
   // softmax latencies (measured: 4K prefill 593 vs 650 µs, 32-token decode
-  // split kernel 19.3 vs 20.4 µs). The fp8 staging registers only fit 4 waves.
-  if (nw == 8 && fp8) nw = 4;
-  if (nw <= 0) nw = (hw >= 2 && !fp8) ? 8 : 4;
+  // split kernel 19.3 vs 20.4 µs). With fp8 rows the 64-head 8-wave build
+  // spills (the staging registers beside the scale groups): 4 waves there.
+  if (nw <= 0) nw = (hw == 2 || (hw == 4 && !fp8)) ? 8 : 4;
   if (nw != 4 && nw != 8) return sas::set_error(SAS_EINVAL, "waves must be 4 or 8");
   if (hw == 1 || pl->exact) nw = 4;
   pl->nw = nw;
@@ -1535,13 +1589,17 @@ int dispatch_hw(int hw, int nw, bool exact, const FwdParams& fp, int nb, hipStre
     if (hw == 4) return launch_fwd<4, 4, D, QT, KVF, true>(fp, nb, st);
     return sas::set_error(SAS_EINVAL, "unsupported head grouping");
   }
-  if (hw == 1) return launch_dec<D, QT, KVF>(fp, nb, st);
+  // 16-head groups: the register-streamed decode kernel, or for fp8 rows
+  // (whose scales are applied per 128-channel group in the LDS kernels) the
+  // 4-wave streaming kernel
+  if (hw == 1) {
+    if constexpr (KVF) return launch_fwd<1, 4, D, QT, KVF>(fp, nb, st);
+    else return launch_dec<D, QT, KVF>(fp, nb, st);
+  }
   if (hw == 2 && nw == 4) return launch_fwd<2, 4, D, QT, KVF>(fp, nb, st);
   if (hw == 4 && nw == 4) return launch_fwd<4, 4, D, QT, KVF>(fp, nb, st);
-  if constexpr (!KVF) {   // fp8 rows are staged through registers: 4 waves only (make_plan)
-    if (hw == 2 && nw == 8) return launch_fwd<2, 8, D, QT, KVF>(fp, nb, st);
-    if (hw == 4 && nw == 8) return launch_fwd<4, 8, D, QT, KVF>(fp, nb, st);
-  }
+  if (hw == 2 && nw == 8) return launch_fwd<2, 8, D, QT, KVF>(fp, nb, st);
+  if (hw == 4 && nw == 8) return launch_fwd<4, 8, D, QT, KVF>(fp, nb, st);
   return sas::set_error(SAS_EINVAL, "unsupported head grouping");
 }
 

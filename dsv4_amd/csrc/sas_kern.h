@@ -66,17 +66,10 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 // while they are in flight waits for them too.
 #define SAS_GLOBAL __attribute__((address_space(1)))
 typedef unsigned u32x4g __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2g __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint4 gld16(uint64_t a) {
   return __builtin_bit_cast(uint4, *reinterpret_cast<const SAS_GLOBAL u32x4g*>(a));
 }
-__device__ __forceinline__ uint2 gld8(uint64_t a) {
-  return __builtin_bit_cast(uint2, *reinterpret_cast<const SAS_GLOBAL u32x2g*>(a));
-}
 __device__ __forceinline__ float gldf(uint64_t a) { return *reinterpret_cast<const SAS_GLOBAL float*>(a); }
-__device__ __forceinline__ float4 gld16f(uint64_t a) {
-  return __builtin_bit_cast(float4, *reinterpret_cast<const SAS_GLOBAL u32x4g*>(a));
-}
 
 static __shared__ __attribute__((aligned(16))) uint4 lds_ring[kLdsRows * kChunksMax];  // 147,456 B
 // compacted rows of the workgroup: the byte address of each cache row
@@ -84,6 +77,9 @@ static __shared__ uint64_t lds_rows[kMaxSlots];
 static __shared__ int lds_cnt[kRoundsMax][kMaxWaves];
 static __shared__ float lds_ml[kMaxWaves][2][16];
 static __shared__ int lds_tok[2];   // resolve(): the token's batch and padded flag
+// fp8 rows: the fp32 scale of each ring row's four 128-channel latent groups
+// ([group][ring row]; the ring holds the unscaled e4m3 values, exact in bf16)
+static __shared__ __attribute__((aligned(16))) float lds_fsc[4][kLdsRows];
 
 struct FwdParams {
   const uint8_t* q;

