@@ -313,20 +313,29 @@ struct Fwd {
     }
     constexpr int kPfK = C::PFK;
     constexpr int RT = C::Q2 ? 1 : MT;   // K row tiles read per k-step
+    // k-step order: fp8 rows interleave the k-steps of two scale groups
+    // (0, 4, 1, 5, 2, 6, 3, 7, then the next pair), so consecutive MFMAs feed
+    // the two group chains alternately; else k-step i is the i-th.
+    auto kord = [](int i) {
+      if (!KVF || i >= 4 * C::NLG) return i;
+      const int j = i & 7;
+      return (i & ~7) + (j & 1) * 4 + (j >> 1);
+    };
     uint4 af[kPfK][RT];
 #pragma unroll
     for (int i = 0; i < kPfK; ++i)
 #pragma unroll
-      for (int mt = 0; mt < RT; ++mt) af[i][mt] = kfrag(i, mt);
+      for (int mt = 0; mt < RT; ++mt) af[i][mt] = kfrag(kord(i), mt);
     // even / odd k-steps accumulate separately: 2 MT independent MFMA chains
 #pragma unroll
-    for (int ks = 0; ks < C::KSQ; ++ks) {
+    for (int i = 0; i < C::KSQ; ++i) {
+      const int ks = kord(i);
       uint4 a[RT];
 #pragma unroll
-      for (int mt = 0; mt < RT; ++mt) a[mt] = af[ks % kPfK][mt];
-      if (ks + kPfK < C::KSQ) {
+      for (int mt = 0; mt < RT; ++mt) a[mt] = af[i % kPfK][mt];
+      if (i + kPfK < C::KSQ) {
 #pragma unroll
-        for (int mt = 0; mt < RT; ++mt) af[ks % kPfK][mt] = kfrag(ks + kPfK, mt);
+        for (int mt = 0; mt < RT; ++mt) af[i % kPfK][mt] = kfrag(kord(i + kPfK), mt);
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -346,13 +355,16 @@ struct Fwd {
         }
       }
       if constexpr (KVF) {
-        if (ks < 4 * C::NLG && ks % 4 == 3) {
+        // a pair of groups complete: fold both into S
+        if (i < 4 * C::NLG && i % 8 == 7) {
+          const int lg = i / 4 - 1;   // the pair's first group
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) sacc[mt] += fs[ks / 4][C::Q2 ? 0 : mt] * gacc[(ks / 4) & 1][mt];
+          for (int mt = 0; mt < MT; ++mt)
+            sacc[mt] += fs[lg][C::Q2 ? 0 : mt] * gacc[0][mt] + fs[lg + 1][C::Q2 ? 0 : mt] * gacc[1][mt];
         }
       }
-      if ((ks & 1) && ks / 2 < C::OPS) dma(ks / 2);
-      if constexpr (kMid) mid(ks);
+      if ((i & 1) && i / 2 < C::OPS) dma(i / 2);
+      if constexpr (kMid) mid(i);
     }
     // schedule: the prefetch reads first, then per k-step MT MFMAs + RT reads
     // (+ a share of the other step's VALU work). Placed before the remaining

@@ -192,6 +192,21 @@ def test_fp8_rows_every_layout_few_and_many_keys(hw, waves, splits):
     _check_baseline(out, lse, ref_out, ref_lse, f"fp8 hw{hw} waves{waves} splits {splits}->{ns}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("hw,waves", [(1, 4), (1, 8), (2, 4), (2, 8), (4, 4), (4, 8)])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_few_keys_every_layout(dtype, hw, waves, splits):
+    """Caches in the query dtype, tokens of 1 to 40 keys beside long rows,
+    through every workgroup layout (16 heads with 4 waves: the exact or
+    streaming schedule; with 8: the register-streamed decode kernel; 32 and
+    64 heads with 4 and 8 waves): the LSE of a one-key token is that key's
+    score merged with the sink, so any error in S shows undiluted."""
+    inp = _small(B=4, H=128, q_lens=[1, 3, 2, 5], kv_lens=[1, 40, 700, 3000], K=200, dtype=dtype)
+    out, lse, ns = _run(inp, num_splits=splits, head_waves=hw, waves=waves)
+    ref_out, ref_lse = _oracle(inp)
+    _check_baseline(out, lse, ref_out, ref_lse, f"{dtype} hw{hw} waves{waves} splits {splits}->{ns}")
+
+
 # ---------------------------------------------------------------------------
 # the reference suite's scenarios (same data as its _build_case)
 # ---------------------------------------------------------------------------
