@@ -607,7 +607,12 @@ def prepare_sparse_attn_sharedkv_backward(dout: torch.Tensor, q: torch.Tensor, o
     and allocate its (zeroed) gradient buffers."""
     kwargs.pop("return_softmax_lse", None)
     call = prepare_sparse_attn_sharedkv(q, **kwargs)
-    a = call.args
+    # a copy: the forward's resolved split count stays with the forward. The
+    # backward takes the caller's count, or plans its own (0); the forward's
+    # plan (C2: 4 splits, 128 workgroups of 64 heads) would leave half the
+    # CUs idle.
+    a = _lib.SasFwdArgs.from_buffer_copy(call.args)
+    a.num_splits = int(kwargs.get("num_splits", 0))
     if a.kv_dtype != a.q_dtype:
         raise ValueError("the backward needs caches in the query dtype (fp8 rows are not differentiated)")
     T1, H = int(a.T), int(a.H)

@@ -629,7 +629,10 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   fp.cmp_ratio = std::max(1, a->cmp_ratio); fp.win_left = a->win_left;
   fp.scale_log2 = a->softmax_scale * kLog2e;
   // KV splits: the caller's count, else enough (token, head group, split)
-  // workgroups for two per CU, each split at least 64 slots
+  // workgroups to fill the CUs, each split at least 128 slots (C2, 640 slots
+  // per token, 32 tokens: 2 / 3 / 4 / 5 / 6 / 8 / 10 splits 110 / 89 / 79 /
+  // 78 / 78 / 84 / 106 µs: below ~128 slots a workgroup's fixed cost and the
+  // extra dq adds outweigh the CUs it adds)
   // 64 heads per workgroup when H allows, else two 16-head groups (each
   // doubling halves the dkv atomics)
   const bool b64 = SAS_BWD64 && a->H % 64 == 0;
@@ -642,7 +645,7 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
     const long long items = a->T * fp.nhg;
     const long long wgs = ng == 1 ? 2LL * device_cus() : (long long)device_cus();
     const long long want = (wgs + items - 1) / items;
-    ns = (int)std::min<long long>(want, (nslots + 63) / 64);
+    ns = (int)std::min<long long>(want, std::max<long long>(1, nslots / 128));
   }
   ns = std::max(1, std::min(ns, 64));
   long long sps = (nslots + ns - 1) / ns;
