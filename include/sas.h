@@ -209,7 +209,8 @@ int sas_combine_v1(const SasCombineArgs* a, void* stream);
  * q, caches (in the query dtype; fp8 rows are not differentiated), tables,
  * indices, seqlens, sinks, and its outputs `out` / `lse`, which are inputs
  * here; its workspace / head-group / wave fields are ignored, num_splits
- * (> 0) sets the KV split count (0: chosen for >= 2 workgroups per CU). Over the forward's
+ * (> 0) sets the KV split count (0: chosen to fill the CUs with splits of
+ * at least 128 key slots; the forward's own plan does not carry over). Over the forward's
  * key set J of each (token, head), with P_j = exp(scale q.k_j - lse),
  * Delta = dout . out, dS_j = P_j (dout . v_j - Delta):
  *   dq = scale sum_j dS_j k_j                      (zero on entry; written or accumulated)
