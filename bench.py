@@ -359,9 +359,12 @@ def bench_decode_configs(names, steps, flush):
         us = ms * 1e3
         byts = rows * rb
         gbs = byts / (us * 1e-6) / 1e9
+        # every head of a token attends its rows: 2 x (576 + 512) FLOP per (row, head)
+        flop = rows * cfg.H * 2 * (cfg.D + cfg.DV)
         res[name] = dict(workload=cfg.notes, tokens=inp.T, gathered_rows=rows, row_bytes=rb,
                          gathered_bytes=byts, us_per_call=round(us, 3), gbs=round(gbs, 1),
-                         hbm_frac=round(gbs / HBM_PEAK_GBS, 4), splits=call.num_splits,
+                         hbm_frac=round(gbs / HBM_PEAK_GBS, 4), useful_flop=flop,
+                         mfma_frac=round(flop / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4), splits=call.num_splits,
                          timing="median of per-call events, caches flushed before each call")
         log(f"{name}: {us:.2f} us/call (cold), {gbs:.0f} GB/s on {byts} gathered bytes, "
             f"splits {call.num_splits}")
