@@ -47,6 +47,7 @@
 #define SAS_PFV 4   // V^T operand channel tiles read ahead (32-row steps)
 #endif
 
+
 namespace sas {
 namespace {
 
@@ -217,24 +218,24 @@ struct Fwd {
   }
 
   // -- fp8 rows: global -> registers, dequantised into a slot on store -------
+  // Every lane issues the same two loads whatever its chunk (latent or rope,
+  // inside the step or not): a 16-byte load at a per-lane offset and the
+  // scale of its latent group. (Loads into the same registers under
+  // divergent latent / rope branches made the compiler wait for every load
+  // in flight between the branches, s_waitcnt vmcnt(0), so a step's fetch
+  // took several round trips.) Lanes past the step's rows repeat its last
+  // row (masked out of the softmax; a real row keeps P.V finite), lanes past
+  // the step's chunks load its first row and store nothing.
   __device__ __forceinline__ void fload(int step) {
     const int rp = rbeg + step * C::TR;
-    const int nk = min(C::TR, nrows - step * C::TR);
+    const int nk = min(C::TR, nrows - step * C::TR);   // >= 1 for every loaded step
 #pragma unroll
     for (int k = 0; k < C::FOPS; ++k) {
       const int e = gt + k * C::GT;
       const int r = e / C::FCPR, c = e - r * C::FCPR;
-      fbuf[k] = make_uint4(0, 0, 0, 0);
-      fsc[k] = 0.f;
-      if (e < C::TR * C::FCPR && r < nk) {
-        const uint64_t src = lds_rows[rp + r];
-        if (c < 32) {
-          fbuf[k] = gld16(src + c * 16);
-          fsc[k] = gldf(src + 512 + 4 * (c >> 3));
-        } else {
-          fbuf[k] = gld16(src + 528 + (c - 32) * 16);
-        }
-      }
+      const uint64_t src = lds_rows[rp + (e < C::TR * C::FCPR ? min(r, nk - 1) : 0)];
+      fbuf[k] = gld16(src + (c < 32 ? c * 16 : 528 + (c - 32) * 16));
+      fsc[k] = gldf(src + 512 + 4 * ((c & 31) >> 3));
     }
   }
   __device__ __forceinline__ void fstore(int j) {

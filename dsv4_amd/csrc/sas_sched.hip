@@ -43,8 +43,10 @@ constexpr int kRowsMax = 5120;   // rows whose figures stay in LDS
 constexpr i64 kMaxRows = i64(1) << 22;   // rows in all
 // The assignment's row scan past a batch's last row: stopped (and reported)
 // after this many rows without blocks. The host scans up to 2^26 rows before
-// it reports the same failure.
-constexpr i64 kDevRowSkip = i64(1) << 16;
+// it reports the same failure; here the bound is the row count itself, so
+// within the 2^22 rows above the device reports the failure exactly where
+// the host does.
+constexpr i64 kDevRowSkip = kMaxRows;
 // rows the row phase takes one at a time before it scans windows
 constexpr int kSeqRows = 1;
 

@@ -23,6 +23,9 @@ from . import _lib
 AIC_CORE_NUM = 36
 AIV_CORE_NUM = 72
 SAS_META_SIZE = 1024
+# batches the device scheduler holds (sas_sched.hip: kMaxB); larger batch
+# counts take the host scheduler
+DEVICE_MAX_BATCHES = 1024
 
 FA_METADATA_SIZE = 8
 FD_METADATA_SIZE = 8
@@ -114,6 +117,20 @@ def _metadata_device(dev, tensors, **scalars) -> torch.Tensor:
     return out
 
 
+def _batch_count(layout_q, cu_seqlens_q, seqused_q, batch_size) -> int:
+    """The scheduler's batch count from tensor sizes only (no device read):
+    seqused_q's length, else cu_seqlens_q's minus one under TND, else
+    ``batch_size`` (metadata.py:345-350; the same rule as both entry
+    points)."""
+    def n(t):
+        return 0 if t is None else (t.numel() if isinstance(t, torch.Tensor) else len(t))
+    if n(seqused_q) > 0:
+        return n(seqused_q)
+    if (layout_q or "BSND") == "TND" and n(cu_seqlens_q) > 0:
+        return n(cu_seqlens_q) - 1
+    return int(batch_size)
+
+
 def sparse_attn_sharedkv_metadata(
     *,
     num_heads_q: int,
@@ -145,13 +162,23 @@ def sparse_attn_sharedkv_metadata(
     """Return the scheduler's INT32 ``[SAS_META_SIZE]`` tensor (CPU, or on
     ``device`` when given), as metadata.py:1018-1086 does.
 
-    When ``device`` is a GPU and every sequence-length tensor given lives on
-    it, the schedule is computed there (``sas_metadata_device_v1``: one
-    kernel on the current stream, no host copy, no synchronisation), bit for
-    bit the host schedule; else on the host (``sas_metadata_v1``)."""
+    When ``device`` is a GPU, every sequence-length tensor given lives on it
+    and the batch count (from the tensors' sizes or ``batch_size``, known
+    without reading them) is at most ``DEVICE_MAX_BATCHES``, the schedule is
+    computed there (``sas_metadata_device_v1``: one kernel on the current
+    stream, no host copy, no synchronisation), bit for bit the host
+    schedule; else on the host (``sas_metadata_v1``).
+
+    The device path cannot raise on values it never reads back: where the
+    host scheduler raises ``ValueError`` for the lengths given (a row scan
+    past a batch's last row that finds no work), or where they exceed the
+    device scheduler's own bound (more than 2^22 query rows in all), the
+    returned tensor holds ``-1`` in element 0 and zeros elsewhere. Element 0
+    of a valid schedule is the first core's enable flag, 0 or 1."""
     tensors = (cu_seqlens_q, cu_seqlens_ori_kv, cu_seqlens_cmp_kv, seqused_q, seqused_kv)
     dev = torch.device(device) if device is not None else None
     if (dev is not None and dev.type == "cuda"
+            and _batch_count(layout_q, cu_seqlens_q, seqused_q, batch_size) <= DEVICE_MAX_BATCHES
             and all(isinstance(t, torch.Tensor) for t in tensors if t is not None)
             and any(t is not None for t in tensors)
             and all(t.is_cuda for t in tensors if t is not None)):

@@ -118,3 +118,23 @@ def test_device_scheduler_at_benchmark_shapes(name):
     torch.cuda.synchronize()
     print(f"[metadata] {name}: {sum(ql)} query rows, device schedule {e0.elapsed_time(e1) * 100:.1f} us per call",
           flush=True)
+
+
+@pytest.mark.parametrize("batches", [1024, 1025, 3000])
+def test_device_lengths_beyond_the_device_batch_bound_take_the_host(batches):
+    """More batches than the device scheduler holds (1024): the call with
+    device-resident lengths still returns the host schedule, on the device,
+    instead of raising; at the bound itself the device computes it."""
+    rnd = random.Random(batches)
+    ql = [rnd.choice([1, 2, 4]) for _ in range(batches)]
+    kl = [rnd.randint(1, 40000) for _ in range(batches)]
+    cu = [0]
+    for x in ql:
+        cu.append(cu[-1] + x)
+    kw = dict(num_heads_q=64, num_heads_kv=1, head_dim=576, batch_size=batches, max_seqlen_q=4,
+              max_seqlen_kv=max(kl), layout_q="TND", cu_seqlens_q=torch.tensor(cu, dtype=torch.int32),
+              seqused_kv=torch.tensor(kl, dtype=torch.int32), cmp_ratio=4, cmp_topk=512)
+    host = sparse_attn_sharedkv_metadata(**kw).tolist()
+    got = sparse_attn_sharedkv_metadata(**_on_device(kw))
+    assert got.is_cuda and got.dtype == torch.int32
+    assert got.cpu().tolist() == host
