@@ -27,9 +27,14 @@ pytestmark = pytest.mark.gpu
 
 OUT_TOL = 2e-2
 LSE_ATOL = 1e-3
+# elements beyond 2e-2 of golden: at most FAR_MUL x golden's own count
+# against its fp64-score twin + FAR_ADD (the twin count itself moves with
+# the host's fp32 summation order: 1 to 3 of 33.5 M on the reference's
+# scfa_prefill@1024)
+FAR_MUL, FAR_ADD = 2, 8
 
 
-def _oracle(inp: cases.Inputs, tokens=None, exact=False):
+def _oracle(inp: cases.Inputs, tokens=None, exact=False, scores_fp64=False):
     c = inp.cfg
     return O.golden_paged(
         inp.q, ori_kv=inp.ori_kv, ori_block_table=inp.ori_bt, cu_seqlens_q=inp.cu_seqlens_q,
@@ -38,7 +43,8 @@ def _oracle(inp: cases.Inputs, tokens=None, exact=False):
         cmp_block_table=inp.cmp_bt if c.scenario >= 2 else None,
         cmp_sparse_indices=inp.cmp_idx if c.scenario == 3 else None,
         cmp_ratio=c.cmp_ratio, ori_win_left=c.win_left, dv=512,
-        dequant=paged.dequantize_kv_fp8 if c.fp8 else None, tokens=tokens, exact=exact)
+        dequant=paged.dequantize_kv_fp8 if c.fp8 else None, tokens=tokens, exact=exact,
+        scores_fp64=scores_fp64)
 
 
 def _run(inp: cases.Inputs, num_splits=0, **kw):
@@ -248,8 +254,16 @@ def test_reference_scenarios(name, s1, dtype):
     torch.testing.assert_close(lse, ref_lse, atol=LSE_ATOL, rtol=0.0,
                                msg=lambda m: f"{name} lse vs golden: {m}")
     _check_baseline(out, lse, ex_out, ex_lse.float(), f"{name} {dtype} vs fp64")
-    far = (out.float() - ref_out.float()).abs() > OUT_TOL + OUT_TOL * ref_out.float().abs()
-    print(f"[parity] {name}: {int(far.sum())} of {far.numel()} elements beyond 2e-2 of golden", flush=True)
+    # Elements beyond 2e-2 of golden itself: bounded by golden's own count
+    # against its twin that sums q k^T in fp64 (same fp32 walk otherwise),
+    # so a regression toward golden's cancellation points fails here
+    # instead of only being printed.
+    far = int(((out.float() - ref_out.float()).abs() > OUT_TOL + OUT_TOL * ref_out.float().abs()).sum())
+    twin_out, _ = _oracle(inp, scores_fp64=True)
+    far_twin = int(((twin_out.float() - ref_out.float()).abs() > OUT_TOL + OUT_TOL * ref_out.float().abs()).sum())
+    print(f"[parity] {name}: {far} of {out.numel()} elements beyond 2e-2 of golden (golden's fp64-score "
+          f"twin: {far_twin})", flush=True)
+    assert far <= FAR_MUL * far_twin + FAR_ADD, f"{name}: {far} elements beyond 2e-2 of golden (twin: {far_twin})"
     if dtype == torch.bfloat16:
         rules = [(out, ref_out, 0.0078125, 1e-4, "out"), (lse, ref_lse, 0.015, 0.005, "lse")]
     else:
@@ -260,15 +274,29 @@ def test_reference_scenarios(name, s1, dtype):
         _check_reference_rule(real, expt, rt, at, f"{name} {what}")
 
 
-def test_reference_scenario_8k_prefill():
-    """scfa_prefill at its full 8192 tokens, every token checked against the
-    oracle: the reference's rule and the BASELINE tolerance."""
-    inp = cases.ref_case("scfa_prefill", dtype=torch.bfloat16)
+REF_8K = [(n, d) for n in ("scfa_prefill", "swa_prefill", "cfa_prefill")
+          for d in (torch.bfloat16, torch.float16)]
+
+
+@pytest.mark.parametrize("name,dtype", REF_8K, ids=[f"{n}-{'bf16' if d == torch.bfloat16 else 'fp16'}"
+                                                    for n, d in REF_8K])
+def test_reference_scenario_8k_prefill(name, dtype):
+    """The reference suite's prefill scenarios at their full 8192 tokens
+    (test_sparse_attn_sharedkv.py:105-109, 151-155, 197-201; bf16 and fp16
+    as its e2e runs, :586-605), every token checked against the oracle:
+    the reference's rule for the dtype and the LSE within 1e-3."""
+    inp = cases.ref_case(name, dtype=dtype)
     out, lse, _ = _run(inp)
     ref_out, ref_lse = _oracle(inp)
-    _check_reference_rule(out, ref_out, 0.0078125, 1e-4, "scfa_prefill out")
-    _check_reference_rule(lse, ref_lse, 0.015, 0.005, "scfa_prefill lse")
-    torch.testing.assert_close(lse, ref_lse, atol=LSE_ATOL, rtol=0.0)
+    if dtype == torch.bfloat16:
+        rules = [(out, ref_out, 0.0078125, 1e-4, "out"), (lse, ref_lse, 0.015, 0.005, "lse")]
+    else:
+        rules = [(out, ref_out, 0.005, 2.5e-5, "out"), (lse, ref_lse, 0.01, 0.001, "lse")]
+    for real, expt, rt, at, what in rules:
+        pct, worst, n_err = _reference_rule(real, expt, rt, at)
+        print(f"[parity] {name} 8K {dtype} {what}: {pct:.3f}% within, worst {worst:.3f}", flush=True)
+        _check_reference_rule(real, expt, rt, at, f"{name} {what}")
+    torch.testing.assert_close(lse, ref_lse, atol=LSE_ATOL, rtol=0.0, msg=lambda m: f"{name} lse: {m}")
 
 
 def test_api_return_type():
