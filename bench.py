@@ -122,22 +122,36 @@ def measured_peaks():
     ms, _ = time_launches(lambda i, st: torch.matmul(a, b, out=c), 1, 20, 3)
     gemm_tf = 2 * m ** 3 / (ms / 20 * 1e-3) / 1e12
     del a, b, c
-    # fp32 atomic adds (the backward's row gradients): index_add_ of 2^17
-    # random 576-float rows into 6144 rows (the C3 cache's row count)
-    rows, n = 6144, 1 << 17
-    g = torch.Generator(device="cuda").manual_seed(5)
+    # fp32 atomic adds (the backward's row gradients): the library's
+    # microbenchmark kernel (each wave adds to a 256-byte run of a row, the
+    # backward's pattern; 2048 x 256 threads x 256 adds into 6144 rows of 576
+    # floats, the C3 cache's shape), and torch's index_add_ of 2^17 random
+    # 576-float rows for comparison. The peak is the larger of the two.
+    import ctypes
+    from dsv4_amd import _lib
+    L = _lib.lib()
+    rows, wgs, iters = 6144, 2048, 256
     dst = torch.zeros(rows, 576, device="cuda")
+    def kern(i, st):
+        _lib.check(L.sas_bench_atomic_add_v1(ctypes.c_void_p(dst.data_ptr()), rows, 576, wgs, iters,
+                                             ctypes.c_void_p(st.cuda_stream)), "sas_bench_atomic_add_v1")
+    ms, _ = time_launches(kern, 1, 10, 2)
+    kern_g = wgs * 256 * iters / (ms / 10 * 1e-3) / 1e9
+    n = 1 << 17
+    g = torch.Generator(device="cuda").manual_seed(5)
     src = torch.randn(n, 576, device="cuda", generator=g)
     idx = torch.randint(0, rows, (n,), device="cuda", generator=g)
     ms, _ = time_launches(lambda i, st: dst.index_add_(0, idx, src), 1, 10, 2)
-    atom_g = n * 576 / (ms / 10 * 1e-3) / 1e9
+    ia_g = n * 576 / (ms / 10 * 1e-3) / 1e9
     del dst, src, idx
     torch.cuda.synchronize()
     return dict(hbm_spec_gbs=HBM_PEAK_GBS, hbm_copy_measured_gbs=round(copy_gbs, 1),
                 bf16_spec_tflops=BF16_PEAK_TFLOPS, bf16_gemm_measured_tflops=round(gemm_tf, 1),
-                fp32_atomic_measured_g_per_s=round(atom_g, 1),
+                fp32_atomic_measured_g_per_s=round(max(kern_g, ia_g), 1),
+                fp32_atomic_kernel_g_per_s=round(kern_g, 1), fp32_atomic_index_add_g_per_s=round(ia_g, 1),
                 how="copy: torch copy_ of 2 GiB (read + write bytes); gemm: torch.matmul 8192^3 bf16; "
-                    "atomics: torch index_add_ of 2^17 x 576 fp32 into 6144 rows")
+                    "atomics: the larger of sas_bench_atomic_add_v1 (2048 x 256 threads x 256 adds, "
+                    "256-byte runs into 6144 x 576 fp32) and torch index_add_ of 2^17 x 576 fp32")
 
 
 def usable_cores():
@@ -411,7 +425,8 @@ def bench_backward(dec_inp, pre_inp, atomic_peak=None):
         res[key] = dict(workload=inp.cfg.name, us_per_call=round(us, 1), useful_flop=flop,
                         tflops=round(tfl, 2), mfma_frac=round(tfl / BF16_PEAK_TFLOPS, 5),
                         heads_per_workgroup=hpw, fp32_row_atomics=atomics, atomic_g_per_s=round(rate, 1),
-                        atomic_frac=round(rate / atomic_peak, 3) if atomic_peak else None)
+                        atomic_frac=round(rate / atomic_peak, 3) if atomic_peak else None,
+                        atomic_frac_of="peaks.fp32_atomic_measured_g_per_s")
         del pb, out, lse, dout
     return res
 

@@ -20,7 +20,8 @@ SAS_META_SIZE = 1024
 SAS_FWD_NO_COMBINE = 1
 
 EXPORTED = ("sas_metadata_v1", "sas_metadata_device_v1", "sas_fwd_plan", "sas_fwd_v1", "sas_fwd_noalloc_v1", "sas_combine_v1",
-            "sas_cache_write_v1", "sas_bwd_v1", "sas_last_error", "sas_version")
+            "sas_cache_write_v1", "sas_bwd_v1", "sas_last_error", "sas_version",
+            "sas_bench_atomic_add_v1")
 
 _i32p = C.POINTER(C.c_int32)
 
@@ -121,6 +122,9 @@ def lib() -> C.CDLL:
                 L.sas_bwd_v1.restype = C.c_int
                 L.sas_cache_write_v1.argtypes = [C.POINTER(SasCacheWriteArgs), C.c_void_p]
                 L.sas_cache_write_v1.restype = C.c_int
+                L.sas_bench_atomic_add_v1.argtypes = [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                                      C.c_void_p]
+                L.sas_bench_atomic_add_v1.restype = C.c_int
                 L.sas_last_error.argtypes = []
                 L.sas_last_error.restype = C.c_char_p
                 L.sas_version.argtypes = []

@@ -103,12 +103,23 @@ def _stage(parts, device, stream) -> torch.Tensor:
 
 
 # split-KV workspaces, one growing buffer per (device, stream): the calls of
-# one stream run in order, so they can share it
-_workspaces = {}
+# one stream run in order, so they can share it. At most _WS_MAX streams keep
+# one (least recently used first out); a dropped or outgrown buffer returns
+# to torch's caching allocator on its own stream, which orders its next use
+# after the kernels already queued there.
+_WS_MAX = 16
+_workspaces = OrderedDict()
 _ws_lock = threading.Lock()
 
 
 def _workspace(device, stream, nbytes: int) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        # A captured call bakes the buffer's address into the graph: it gets
+        # its own, from the graph's private pool (kept for the graph's
+        # lifetime), never the shared per-stream buffer that a later, larger
+        # eager call may replace and free.
+        with torch.cuda.stream(stream):
+            return torch.empty(nbytes, dtype=torch.uint8, device=device)
     key = (device, stream.cuda_stream)
     with _ws_lock:
         ws = _workspaces.get(key)
@@ -116,6 +127,9 @@ def _workspace(device, stream, nbytes: int) -> torch.Tensor:
             with torch.cuda.stream(stream):
                 ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
             _workspaces[key] = ws
+        _workspaces.move_to_end(key)
+        while len(_workspaces) > _WS_MAX:
+            _workspaces.popitem(last=False)
     return ws
 
 

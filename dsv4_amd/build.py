@@ -27,7 +27,7 @@ HIP_FLAGS = [
 # keep MFMA accumulators in arch VGPRs: with AGPR accumulators the register
 # allocator inserts AGPR<->VGPR copies on every loop back-edge
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-SOURCES = [("sas_fwd.hip", VGPR_FORM), ("sas_bwd.hip", []), ("sas_cache.hip", []), ("sas_sched.hip", []), ("sas_metadata.cpp", []), ("sas_error.cpp", [])]
+SOURCES = [("sas_fwd.hip", VGPR_FORM), ("sas_bwd.hip", []), ("sas_cache.hip", []), ("sas_sched.hip", []), ("sas_metadata.cpp", []), ("sas_error.cpp", []), ("sas_bench.hip", [])]
 
 
 def hipcc() -> str:

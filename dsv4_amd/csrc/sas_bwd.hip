@@ -588,9 +588,9 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   if (a->scenario < SAS_SWA || a->scenario > SAS_SCFA) return set_error(SAS_EINVAL, "bwd: bad scenario");
   if (a->q_dtype != SAS_DT_BF16 && a->q_dtype != SAS_DT_FP16) return set_error(SAS_EINVAL, "bwd: q dtype");
   if (a->kv_dtype != a->q_dtype) return set_error(SAS_EINVAL, "bwd: the cache must be in the query dtype (no fp8 rows)");
-  if (a->win_left < 0 || a->win_left > 8191) return set_error(SAS_EINVAL, "bwd: win_left out of range");
+  if (a->win_left < 0) return set_error(SAS_EINVAL, "bwd: win_left out of range");
   if (a->scenario >= SAS_CFA && (a->cmp_ratio < 1 || a->K < 0)) return set_error(SAS_EINVAL, "bwd: bad cmp_ratio/K");
-  const long long nslots = a->win_left + 1 + (a->scenario >= SAS_CFA ? a->K : 0);
+  const long long nslots = (long long)a->win_left + 1 + (a->scenario >= SAS_CFA ? a->K : 0);
   if (a->T == 0) return SAS_OK;
   if (!a->q || !a->ori_kv || !a->ori_block_table || !a->q_prefix || !a->act_kv || !a->sinks ||
       !a->out || !a->lse || !ba->dout || !ba->dq || !ba->d_ori_kv || !ba->d_sinks)
@@ -647,13 +647,17 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
     const long long want = (wgs + items - 1) / items;
     ns = (int)std::min<long long>(want, std::max<long long>(1, nslots / 128));
   }
-  ns = std::max(1, std::min(ns, 64));
+  // at most 64 splits of the planner's own choice; up to kMaxBwdSplits when
+  // the token's slots need them or the caller asks
+  constexpr long long kMaxBwdSplits = 1 << 16;
+  ns = (int)std::max<long long>(1, std::min<long long>(ns, a->num_splits > 0 ? kMaxBwdSplits : 64));
   long long sps = (nslots + ns - 1) / ns;
   if (sps > kMaxSlots) {
     // a workgroup resolves at most kMaxSlots slots: more splits (dq is then
     // accumulated atomically across them)
-    ns = (int)((nslots + kMaxSlots - 1) / kMaxSlots);
-    if (ns > 64) return set_error(SAS_EINVAL, "bwd: too many key slots per token (%lld)", nslots);
+    const long long need = (nslots + kMaxSlots - 1) / kMaxSlots;
+    if (need > kMaxBwdSplits) return set_error(SAS_EINVAL, "bwd: too many key slots per token (%lld)", nslots);
+    ns = (int)need;
     sps = (nslots + ns - 1) / ns;
   }
   fp.nsplit = (int)((nslots + sps - 1) / sps);
@@ -664,7 +668,9 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   bp.d_ori = ba->d_ori_kv;
   bp.d_cmp = ba->d_cmp_kv;
   bp.d_sinks = ba->d_sinks;
-  const int nblocks = (int)((a->T + kXcds - 1) / kXcds) * fp.nhg * fp.nsplit * kXcds;
+  const long long nblocks_ll = (long long)((a->T + kXcds - 1) / kXcds) * fp.nhg * fp.nsplit * kXcds;
+  if (nblocks_ll > INT_MAX) return set_error(SAS_EINVAL, "bwd: %lld workgroups beyond one launch", nblocks_ll);
+  const int nblocks = (int)nblocks_ll;
   hipStream_t st = (hipStream_t)stream;
   if (b64) {
     if (a->q_dtype == SAS_DT_BF16)

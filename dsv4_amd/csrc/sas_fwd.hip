@@ -1450,7 +1450,13 @@ sas_dec_kernel(const FwdParams p) {
 #define SAS_COMBINE_THREADS 256
 #endif
 constexpr int kCombineThreads = SAS_COMBINE_THREADS;
-constexpr int kMaxCombineSplits = 64;
+// Split counts: the planner's own choice fills the CUs with at most
+// kMaxAutoSplits; a token with more key slots than kMaxAutoSplits x kMaxSlots
+// (long CFA rows, wide windows), or an explicit count, takes up to
+// kMaxSplits. The combine merges any count, kB splits' loads at a time.
+constexpr int kMaxAutoSplits = 64;
+constexpr int kMaxSplits = 1 << 16;
+constexpr long long kMaxTokenSlots = (long long)kMaxSplits * kMaxSlots;
 
 // One workgroup per (token, 4 heads), thread = (head, 8 channels): 16-byte
 // fp16 partial loads (C2 call 19.95 -> 19.7 us against 4 channels).
@@ -1490,9 +1496,13 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   if (a->H % 16) return sas::set_error(SAS_EINVAL, "H must be a multiple of 16 (got %lld)", (long long)a->H);
   if (a->scenario < SAS_SWA || a->scenario > SAS_SCFA) return sas::set_error(SAS_EINVAL, "bad scenario");
   if (a->flags & ~SAS_FWD_NO_COMBINE) return sas::set_error(SAS_EINVAL, "unknown flags 0x%x", a->flags);
-  if (a->win_left < 0 || a->win_left > 8191) return sas::set_error(SAS_EINVAL, "win_left out of range");
+  if (a->win_left < 0) return sas::set_error(SAS_EINVAL, "win_left out of range");
   if (a->scenario >= SAS_CFA && (a->cmp_ratio < 1 || a->K < 0)) return sas::set_error(SAS_EINVAL, "bad cmp_ratio/K");
-  pl->nslots = a->win_left + 1 + (a->scenario >= SAS_CFA ? (int)a->K : 0);
+  const long long nslots_ll = (long long)a->win_left + 1 + (a->scenario >= SAS_CFA ? a->K : 0);
+  if (nslots_ll > kMaxTokenSlots)
+    return sas::set_error(SAS_EINVAL, "%lld key slots per token (win_left + 1 + K) beyond %lld", nslots_ll,
+                          kMaxTokenSlots);
+  pl->nslots = (int)nslots_ll;
   const long long T = std::max<long long>(a->T, 1);
   int hw = a->head_waves;
   int ns = a->num_splits;
@@ -1555,20 +1565,20 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
     const int max_by_len = std::max(1, (pl->nslots + min_sps - 1) / min_sps);
     ns = (int)std::min<long long>(one_round_splits(hw), max_by_len);
   }
-  ns = std::max(1, std::min(ns, kMaxCombineSplits));
+  ns = std::max(1, std::min(ns, a->num_splits > 0 ? kMaxSplits : kMaxAutoSplits));
   // 16-head groups run the exact schedule when a split's rows fit the ring
   // (every row gathered at once, no per-step barriers; 1-token, 16-head
   // decode: 12.7 µs against 15.5 µs for the register-streaming decode
   // kernel), taking the splits that make them fit if one round holds them
   if (!pl->exact && hw == 1 && (a->waves == 0 || a->waves == 4)) {
     const int fit = (pl->nslots + kLdsRows - 1) / kLdsRows;
-    if (a->num_splits <= 0 && ns < fit && fit <= std::min<long long>(one_round_splits(1), kMaxCombineSplits)) ns = fit;
+    if (a->num_splits <= 0 && ns < fit && fit <= std::min<long long>(one_round_splits(1), kMaxAutoSplits)) ns = fit;
     pl->exact = (pl->nslots + ns - 1) / ns <= kLdsRows;
   }
   int sps = (pl->nslots + ns - 1) / ns;
   if (sps > kMaxSlots) {
     ns = (pl->nslots + kMaxSlots - 1) / kMaxSlots;
-    if (ns > kMaxCombineSplits) return sas::set_error(SAS_EINVAL, "too many key slots per token");
+    if (ns > kMaxSplits) return sas::set_error(SAS_EINVAL, "too many key slots per token");
     sps = (pl->nslots + ns - 1) / ns;
   }
   ns = (pl->nslots + sps - 1) / sps;  // drop empty trailing splits
@@ -1633,8 +1643,8 @@ int launch_combine(const FwdParams& fp, int out_dtype, hipStream_t st) {
 int combine_impl(const SasCombineArgs* a, hipStream_t st) {
   if (!a || !a->part_o || !a->part_ml || !a->sinks || !a->out || !a->lse)
     return sas::set_error(SAS_EINVAL, "combine: null pointer");
-  if (a->DV != kDV || a->S < 1 || a->S > kMaxCombineSplits || a->H < 1 || a->T < 0)
-    return sas::set_error(SAS_EINVAL, "combine: bad dims (S must be 1..64, DV 512)");
+  if (a->DV != kDV || a->S < 1 || a->S > kMaxSplits || a->H < 1 || a->T < 0)
+    return sas::set_error(SAS_EINVAL, "combine: bad dims (S must be 1..%d, DV 512)", kMaxSplits);
   if (a->T == 0) return SAS_OK;
   FwdParams fp{};
   fp.part_o = (uint8_t*)const_cast<void*>(a->part_o);
@@ -1713,7 +1723,11 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   fp.scale_log2 = a->softmax_scale * kLog2e;
   fp.nsplit = pl.nsplit; fp.slots_per_split = pl.sps; fp.nhg = pl.nhg;
   // item_index(): ceil(T / 8) tokens per XCD, nhg * nsplit workgroups each
-  const int nblocks = (int)((a->T + kXcds - 1) / kXcds) * pl.nhg * pl.nsplit * kXcds;
+  const long long nblocks_ll = (long long)((a->T + kXcds - 1) / kXcds) * pl.nhg * pl.nsplit * kXcds;
+  if (nblocks_ll > INT_MAX)
+    return sas::set_error(SAS_EINVAL, "%lld workgroups (tokens x head groups x splits) beyond one launch",
+                          nblocks_ll);
+  const int nblocks = (int)nblocks_ll;
   // Large partials of a grid that is resident all at once stream out during
   // the kernel instead of leaving the L2 dirty for the writeback at its end
   // (C2 decode: 22.7 -> 22.0 µs); with a second wave of workgroups, or small

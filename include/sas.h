@@ -128,7 +128,10 @@ typedef struct SasFwdArgs {
   int32_t cmp_ratio;
   int32_t win_left;              /* ori_win_left (window = win_left + 1 rows) */
   float softmax_scale;
-  int32_t num_splits;            /* KV splits per token; 0 = choose automatically.
+  int32_t num_splits;            /* KV splits per token, 1..65536; 0 = choose
+                                    automatically (at most 64, more when a token's
+                                    win_left + 1 + K key slots exceed 64 x 1280;
+                                    at most 65536 x 1280 slots per token).
                                     Above 1 on a window-only call, it selects the
                                     streaming schedule over the one-split exact one */
   int32_t head_waves;            /* waves sharing each KV tile (16 heads each): 1, 2, 4;
@@ -196,7 +199,7 @@ typedef struct SasCombineArgs {
   const float* sinks;
   void* out;
   float* lse;
-  int64_t T, S, H, DV;
+  int64_t T, S, H, DV;           /* S: 1..65536 splits */
   int32_t out_dtype;             /* SAS_DT_BF16 or SAS_DT_FP16 */
 } SasCombineArgs;
 

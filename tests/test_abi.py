@@ -1,4 +1,4 @@
-"""C ABI of libsas.so: every function include/sas.h declares is exported, and
+"""C ABI of libsas.so: every function include/*.h declares is exported, and
 argument validation fails with the documented status codes before any
 device work (no GPU needed)."""
 
@@ -12,11 +12,12 @@ import pytest
 
 from dsv4_amd import _lib
 
-HEADER = os.path.join(os.path.dirname(__file__), "..", "include", "sas.h")
+INCLUDE = os.path.join(os.path.dirname(__file__), "..", "include")
+HEADER = os.path.join(INCLUDE, "sas.h")
 
 
 def _declared():
-    text = open(HEADER).read()
+    text = "\n".join(open(os.path.join(INCLUDE, f)).read() for f in sorted(os.listdir(INCLUDE)) if f.endswith(".h"))
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(sas_\w+)\s*\(", text, flags=re.M)))
 
@@ -130,7 +131,7 @@ def test_combine_rejects():
     assert _lib.lib().sas_combine_v1(C.byref(ca), None) == _lib.SAS_EINVAL
     fake = 1 << 40
     ca.part_o = ca.part_ml = ca.sinks = ca.out = ca.lse = fake
-    ca.T, ca.S, ca.H, ca.DV, ca.out_dtype = 1, 65, 64, 512, _lib.SAS_DT_BF16
+    ca.T, ca.S, ca.H, ca.DV, ca.out_dtype = 1, (1 << 16) + 1, 64, 512, _lib.SAS_DT_BF16
     assert _lib.lib().sas_combine_v1(C.byref(ca), None) == _lib.SAS_EINVAL
     assert "S must be" in _lib.lib().sas_last_error().decode()
 
@@ -141,3 +142,14 @@ def test_check_maps_status_to_exceptions():
         _lib.check(_lib.SAS_EINVAL, "x")
     with pytest.raises(RuntimeError):
         _lib.check(_lib.SAS_ELAUNCH, "x")
+
+
+def test_plan_long_rows_take_more_than_64_splits():
+    """A token's key slots beyond 64 splits of 1280 (long CFA rows, wide
+    windows) plan more splits; only beyond 2^16 splits is the call refused."""
+    rc, ns, ws = _plan(_valid_args(scenario=_lib.SAS_CFA, K=200000))
+    assert rc == _lib.SAS_OK and ns >= (200000 + 128 + 1279) // 1280
+    rc, ns, _ = _plan(_valid_args(scenario=_lib.SAS_SWA, K=0, win_left=20000))
+    assert rc == _lib.SAS_OK and ns >= 1
+    rc, _, _ = _plan(_valid_args(scenario=_lib.SAS_CFA, K=(1 << 16) * 1280))
+    assert rc == _lib.SAS_EINVAL

@@ -144,6 +144,10 @@ def _gpu_case(name):
         # 128 + 2048 dense compressed slots per token: beyond one workgroup's
         # 1280-slot range, so the planner splits the key range
         "cfa_2176_slots": dict(B=2, H=16, q_lens=[2, 1], kv_lens=[8192, 6000], K=0, scenario=2, ratio=4),
+        # the same beyond-1280-slot split through the 64-head kernel
+        # (sas_bwd64_kernel: H a multiple of 64), with 64 and 128 heads
+        "cfa_2176_slots_h64": dict(B=2, H=64, q_lens=[2, 1], kv_lens=[8192, 6000], K=0, scenario=2, ratio=4),
+        "cfa_2176_slots_h128": dict(B=2, H=128, q_lens=[1, 2], kv_lens=[7000, 8192], K=0, scenario=2, ratio=4),
     }[name]
     return _small(**spec)
 
@@ -217,7 +221,7 @@ def _oracle_bwd(inp, dout, out, lse, tokens=None):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", ["C1", "scfa_prefill", "swa", "cfa", "fp16_d512", "decode_h64", "short_kv",
-                                  "cfa_2176_slots"])
+                                  "cfa_2176_slots", "cfa_2176_slots_h64", "cfa_2176_slots_h128"])
 def test_gpu_backward_matches_oracle(name):
     from dsv4_amd.api import sparse_attn_sharedkv, sparse_attn_sharedkv_backward
     inp = _gpu_case(name)

@@ -425,6 +425,11 @@ EDGE = {
                               dtype=torch.float16),
     "swa_h32_win63": dict(B=2, H=32, q_lens=[4, 1], kv_lens=[700, 64], K=0, scenario=1, win=63),
     "swa_fp8": dict(B=2, H=64, q_lens=[1, 2], kv_lens=[3000, 90], K=0, scenario=1, fp8=True),
+    # 90,240 dense compressed + window slots per token: beyond 64 splits of
+    # 1280 slots (71 splits), as long CFA contexts need (api.py:257-268)
+    "cfa_beyond_64_splits": dict(B=1, H=16, q_lens=[1], kv_lens=[90000], K=0, scenario=2, ratio=1),
+    # a 9000-row sliding window (win_left = 8999)
+    "swa_window_9000": dict(B=2, H=64, q_lens=[1, 2], kv_lens=[12000, 9500], K=0, scenario=1, win=8999),
     "swa_prefill_h128": dict(B=1, H=128, q_lens=[300], kv_lens=[300], K=0, scenario=1),
     "swa_win200": dict(B=2, H=64, q_lens=[2, 1], kv_lens=[1000, 150], K=0, scenario=1, win=200),
 }
@@ -629,6 +634,32 @@ def test_prepared_call_replays_in_a_hip_graph():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(call.out, ref_out) and torch.equal(call.lse, ref_lse), f"replay {i}"
+
+
+def test_drop_in_call_captured_in_a_graph_keeps_its_workspace():
+    """The drop-in call captured in a HIP graph owns its split workspace: an
+    eager call with a larger workspace on the same stream afterwards (which
+    replaces that stream's shared buffer) leaves the graph's replays equal to
+    the eager result."""
+    small = cases.make_inputs(cases.CONFIGS["C1"], device="cpu").to("cuda")
+    big = cases.make_inputs(cases.CONFIGS["C2"], device="cpu").to("cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ref_out, ref_lse = sparse_attn_sharedkv(small.q, return_softmax_lse=True, **small.api_kwargs())
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            g_out, g_lse = sparse_attn_sharedkv(small.q, return_softmax_lse=True, **small.api_kwargs())
+        for i in range(3):
+            # a larger call on the same stream grows (replaces) its shared workspace
+            b_out = sparse_attn_sharedkv(big.q, **big.api_kwargs())
+            g_out.fill_(float(i + 1))
+            g_lse.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(g_out, ref_out) and torch.equal(g_lse, ref_lse), f"replay {i}"
+            del b_out
 
 
 def test_api_repeated_calls_read_current_values():
