@@ -102,6 +102,116 @@ def _stage(parts, device, stream) -> torch.Tensor:
     return _staging.to_device(parts, device, stream)
 
 
+def _raw_stream(dev: torch.device) -> int:
+    """The current stream of ``dev`` as a hipStream_t value (no Stream object)."""
+    f = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if f is not None:
+        return int(f(dev.index if dev.index is not None else torch.cuda.current_device()))
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _hip_check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed (hipError {rc})")
+
+
+def _hip_runtime():
+    """The HIP runtime entry points of the library libsas.so runs on (the
+    runtime torch loaded), resolved through libsas's handle."""
+    L = _lib.lib()
+    if not getattr(L, "_sas_hip_bound", False):
+        L.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        L.hipMemcpyAsync.restype = C.c_int
+        L.hipEventCreateWithFlags.argtypes = [C.POINTER(C.c_void_p), C.c_uint]
+        L.hipEventCreateWithFlags.restype = C.c_int
+        L.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        L.hipEventRecord.restype = C.c_int
+        L.hipEventSynchronize.argtypes = [C.c_void_p]
+        L.hipEventSynchronize.restype = C.c_int
+        L._sas_hip_bound = True
+    return L
+
+
+class _SeqlenRing:
+    """Host-side sequence lengths of the drop-in call reach the device
+    through two rings of SLOTS slots per device: pinned host memory, filled
+    with memmove, and device memory, filled by one hipMemcpyAsync on the
+    call's stream; no tensor is created per call. A slot is handed out again
+    once the event recorded after the launch that read it (so after its copy
+    and its kernels) has completed; a slot between its copy and that record
+    is skipped."""
+
+    SLOTS, SLOT_INTS = 64, 1024
+    FREE, PENDING, RECORDED = 0, 1, 2
+
+    def __init__(self, device: torch.device):
+        self.host = torch.empty(self.SLOTS * self.SLOT_INTS, dtype=torch.int32, pin_memory=True)
+        self.dev = torch.empty(self.SLOTS * self.SLOT_INTS, dtype=torch.int32, device=device)
+        self.hbase, self.dbase = self.host.data_ptr(), self.dev.data_ptr()
+        self.hip = _hip_runtime()
+        self.events = []
+        with torch.cuda.device(device):
+            for _ in range(self.SLOTS):
+                ev = C.c_void_p()
+                _hip_check(self.hip.hipEventCreateWithFlags(C.byref(ev), 2), "hipEventCreateWithFlags")
+                self.events.append(ev)
+        self.state = [self.FREE] * self.SLOTS
+        self.next = 0
+        self.lock = threading.Lock()
+
+    def stage(self, parts, stream_ptr: int):
+        """Copy the host int32 arrays ``parts`` ((address, count) pairs) into
+        one device slot on the stream. Returns (device address, slot), or
+        None when they do not fit a slot or every slot is pending."""
+        n = sum(cnt for _, cnt in parts)
+        if n > self.SLOT_INTS:
+            return None
+        with self.lock:
+            for _ in range(self.SLOTS):
+                slot = self.next
+                self.next = (slot + 1) % self.SLOTS
+                if self.state[slot] != self.PENDING:
+                    break
+            else:
+                return None
+            if self.state[slot] == self.RECORDED:
+                _hip_check(self.hip.hipEventSynchronize(self.events[slot]), "hipEventSynchronize")
+            self.state[slot] = self.PENDING
+        off = slot * self.SLOT_INTS * 4
+        o = 0
+        for addr, cnt in parts:
+            C.memmove(self.hbase + off + o, addr, 4 * cnt)
+            o += 4 * cnt
+        rc = self.hip.hipMemcpyAsync(self.dbase + off, self.hbase + off, 4 * n, 1, stream_ptr)
+        if rc != 0:
+            with self.lock:
+                self.state[slot] = self.FREE
+            _hip_check(rc, "hipMemcpyAsync")
+        return self.dbase + off, slot
+
+    def release(self, slot: int, stream_ptr: int) -> None:
+        """After the launch that reads the slot: its reuse waits for this."""
+        rc = self.hip.hipEventRecord(self.events[slot], stream_ptr)
+        with self.lock:
+            self.state[slot] = self.RECORDED if rc == 0 else self.FREE
+        _hip_check(rc, "hipEventRecord")
+
+
+_rings = {}
+_rings_lock = threading.Lock()
+
+
+def _seqlen_ring(dev: torch.device) -> _SeqlenRing:
+    key = dev.index
+    ring = _rings.get(key)
+    if ring is None:
+        with _rings_lock:
+            ring = _rings.get(key)
+            if ring is None:
+                ring = _rings[key] = _SeqlenRing(dev)
+    return ring
+
+
 # split-KV workspaces, one growing buffer per (device, stream): the calls of
 # one stream run in order, so they can share it. At most _WS_MAX streams keep
 # one (least recently used first out); a dropped or outgrown buffer returns
@@ -112,20 +222,22 @@ _workspaces = OrderedDict()
 _ws_lock = threading.Lock()
 
 
-def _workspace(device, stream, nbytes: int) -> torch.Tensor:
+def _workspace(device, stream_ptr: int, nbytes: int) -> torch.Tensor:
+    """A workspace of at least ``nbytes`` for a call on ``device``'s current
+    stream (``stream_ptr``)."""
     if torch.cuda.is_current_stream_capturing():
         # A captured call bakes the buffer's address into the graph: it gets
         # its own, from the graph's private pool (kept for the graph's
         # lifetime), never the shared per-stream buffer that a later, larger
         # eager call may replace and free.
-        with torch.cuda.stream(stream):
-            return torch.empty(nbytes, dtype=torch.uint8, device=device)
-    key = (device, stream.cuda_stream)
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    key = (device, stream_ptr)
     with _ws_lock:
         ws = _workspaces.get(key)
         if ws is None or ws.numel() < nbytes:
-            with torch.cuda.stream(stream):
-                ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            # allocated on the current stream (the call's), in the caching
+            # allocator's pool of that stream
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
             _workspaces[key] = ws
         _workspaces.move_to_end(key)
         while len(_workspaces) > _WS_MAX:
@@ -337,16 +449,17 @@ def _resolve(q, *, ori_kv, cmp_kv, cmp_sparse_indices, ori_block_table, cmp_bloc
     return r
 
 
-def _bind_seqlens(r: _Resolved, parts, a: _lib.SasFwdArgs, stream, keep: list) -> None:
-    """Copy the call's host-side sequence lengths ``parts`` ((name, int32
-    tensor) pairs, the names of ``r.host_parts``) to the device through the
-    pinned ring and point the launch arguments at them."""
-    if not parts:
-        return
-    dev = _stage([t for _, t in parts], r.device, stream)
-    keep.append(dev)
+def _host_i32(t: torch.Tensor) -> torch.Tensor:
+    """A host tensor as contiguous int32 (itself when it already is)."""
+    if t.dtype is not torch.int32 or not t.is_contiguous():
+        t = t.to(torch.int32).contiguous()
+    return t
+
+
+def _point_seqlens(parts, a: _lib.SasFwdArgs, base: int) -> None:
+    """Point the launch arguments at ``parts`` ((name, tensor) pairs) laid
+    out one after the other from device address ``base``."""
     o = 0
-    base = dev.data_ptr()
     for name, t in parts:
         ptr = base + 4 * o
         if name == "cu":
@@ -358,6 +471,17 @@ def _bind_seqlens(r: _Resolved, parts, a: _lib.SasFwdArgs, stream, keep: list) -
         else:
             a.act_kv = ptr
         o += int(t.numel())
+
+
+def _bind_seqlens(r: _Resolved, parts, a: _lib.SasFwdArgs, stream, keep: list) -> None:
+    """Copy the call's host-side sequence lengths ``parts`` ((name, int32
+    tensor) pairs, the names of ``r.host_parts``) to the device through the
+    pinned ring and point the launch arguments at them."""
+    if not parts:
+        return
+    dev = _stage([t for _, t in parts], r.device, stream)
+    keep.append(dev)
+    _point_seqlens(parts, a, dev.data_ptr())
 
 
 class PreparedCall:
@@ -542,7 +666,7 @@ def sparse_attn_sharedkv(
     ``lse = max + ln(sum)`` over all attended keys and the sink.
     """
     dev = q.device
-    stream = torch.cuda.current_stream(dev) if q.is_cuda else None
+    stream = _raw_stream(dev) if q.is_cuda else None
     # CFA's slot count follows the longest sequence (api.py:259-261): part of
     # the signature, read from the host copy, or through a sync as the
     # reference does for device lengths
@@ -552,8 +676,7 @@ def sparse_attn_sharedkv(
     key = (_sig(q), _sig(ori_kv), _sig(cmp_kv), _sig(cmp_sparse_indices), _sig(ori_block_table),
            _sig(cmp_block_table), _sig(cu_seqlens_q), _sig(seqused_kv), _sig(sinks),
            None if metadata is None else metadata.numel(), float(softmax_scale), cmp_ratio, ori_mask_mode,
-           cmp_mask_mode, ori_win_left, ori_win_right, layout_q, layout_kv, core_num, topk_cmp, cfa_k,
-           None if stream is None else stream.cuda_stream)
+           cmp_mask_mode, ori_win_left, ori_win_right, layout_q, layout_kv, core_num, topk_cmp, cfa_k, stream)
     with _cache_lock:
         r = _cache.get(key)
         if r is not None:
@@ -577,18 +700,29 @@ def sparse_attn_sharedkv(
     a = _lib.SasFwdArgs.from_buffer_copy(r.args)
     a.out, a.lse = out.data_ptr(), lse.data_ptr()
     keep = []
+    staged = None
     if r.host_parts:
         parts = r.host_parts
         if hit:
             # this call's host lengths (a cached resolution, TND only, holds
             # an earlier call's)
             cur = {"cu": cu_seqlens_q, "kv": seqused_kv}
-            parts = [(name, cur[name].to(torch.int32).reshape(-1)) for name, _ in r.host_parts]
-        _bind_seqlens(r, parts, a, stream, keep)
-    if r.ws_bytes:
-        ws = _workspace(dev, stream, r.ws_bytes)
-        a.workspace, a.workspace_bytes = ws.data_ptr(), r.ws_bytes
-    _lib.check(_lib.lib().sas_fwd_v1(C.byref(a), C.c_void_p(stream.cuda_stream)), "sparse_attn_sharedkv")
+            parts = [(name, _host_i32(cur[name])) for name, _ in r.host_parts]
+        if not torch.cuda.is_current_stream_capturing():
+            ring = _seqlen_ring(dev)
+            staged = ring.stage([(t.data_ptr(), t.numel()) for _, t in parts], stream)
+        if staged is not None:
+            _point_seqlens(parts, a, staged[0])
+        else:
+            _bind_seqlens(r, parts, a, torch.cuda.current_stream(dev), keep)
+    try:
+        if r.ws_bytes:
+            ws = _workspace(dev, stream, r.ws_bytes)
+            a.workspace, a.workspace_bytes = ws.data_ptr(), r.ws_bytes
+        _lib.check(_lib.lib().sas_fwd_v1(C.byref(a), C.c_void_p(stream)), "sparse_attn_sharedkv")
+    finally:
+        if staged is not None:
+            ring.release(staged[1], stream)
     return _result(out, lse, r.layout_q, r.B, r.S_max, return_softmax_lse)
 
 
