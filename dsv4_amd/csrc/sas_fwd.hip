@@ -253,7 +253,7 @@ struct Fwd {
         const uint32_t w[4] = {fbuf[k].x, fbuf[k].y, fbuf[k].z, fbuf[k].w};
         uint32_t o[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e4m3x4_to_bf16(w[i], 1.f, o[2 * i], o[2 * i + 1]);
+        for (int i = 0; i < 4; ++i) e4m3x4_to_bf16(w[i], o[2 * i], o[2 * i + 1]);
         row[(2 * c) ^ sw] = make_uint4(o[0], o[1], o[2], o[3]);
         row[(2 * c + 1) ^ sw] = make_uint4(o[4], o[5], o[6], o[7]);
         if ((c & 7) == 0) lds_fsc[c >> 3][sl / C::CH + r] = fsc[k];

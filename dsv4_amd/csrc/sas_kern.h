@@ -119,16 +119,16 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Four OCP e4m3fn bytes (one dword, byte 0 first) dequantised with `scale`
-// and rounded to bf16 pairs: lo = bytes 0-1, hi = bytes 2-3. gfx950's
-// v_cvt_pk_f32_fp8 decodes OCP e4m3fn (bias 7, subnormals m * 2^-9) exactly,
-// two bytes per instruction; 0x7f / 0xff (NaN) are never written by the
-// cache writer, which saturates at 448.
-__device__ __forceinline__ void e4m3x4_to_bf16(uint32_t w, float scale, uint32_t& lo, uint32_t& hi) {
-  const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-  const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-  lo = pack2<__bf16>(a[0] * scale, a[1] * scale);
-  hi = pack2<__bf16>(b[0] * scale, b[1] * scale);
+// Four OCP e4m3fn bytes (one dword, byte 0 first) as bf16 pairs, unscaled:
+// lo = bytes 0-1, hi = bytes 2-3. gfx950's v_cvt_scalef32_pk_bf16_fp8
+// converts two OCP e4m3fn bytes (bias 7, subnormals m * 2^-9) straight to a
+// bf16 pair; with scale 1 the result is exact (every e4m3fn value is a bf16
+// value). 0x7f / 0xff (NaN) are never written by the cache writer, which
+// saturates at 448.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+  hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
 }
 
 // 16x16x32: A = 8 values of row l%16 (k = 8*(l/16)..), B likewise by column
