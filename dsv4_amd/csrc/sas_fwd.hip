@@ -170,9 +170,17 @@ struct Fwd {
   };
   __device__ __forceinline__ void prep(Dma& d, int j, int step) const {
     const int rp = rbeg + step * C::TR;
-    const int last = rp + min(C::TR, nrows - step * C::TR) - 1;   // nk >= 1 for every issued step
+    if constexpr (C::QL) {
+      // lds_rows holds kRowPad copies of the last row past the compacted
+      // ones, and a step's rows end within them: no clamp
+      const uint64_t* rows = lds_rows + rp;
 #pragma unroll
-    for (int o = 0; o < C::OPS; ++o) d.ra[o] = lds_rows[min(rp + drow(o), last)];
+      for (int o = 0; o < C::OPS; ++o) d.ra[o] = rows[drow(o)];
+    } else {
+      const int last = rp + min(C::TR, nrows - step * C::TR) - 1;   // nk >= 1 for every issued step
+#pragma unroll
+      for (int o = 0; o < C::OPS; ++o) d.ra[o] = lds_rows[min(rp + drow(o), last)];
+    }
     d.lds = lds_addr_of(&lds_ring[slot(j)]);
   }
   __device__ __forceinline__ void fire(const Dma& d, int o) const {
@@ -1220,6 +1228,12 @@ sas_fwd_kernel(const FwdParams p) {
     }
   });
   const int nvalid = __builtin_amdgcn_readfirstlane(k.nvalid);
+  // QL kernels: pad lds_rows with copies of the last row (read after the
+  // query barrier below; with no rows no step is issued)
+  if constexpr (C::QL && !KVF) {
+    static_assert(2 * C::TR <= kRowPad, "a step past the last reaches at most 2 TR entries beyond it");
+    if (tid < kRowPad) lds_rows[nvalid + tid] = lds_rows[nvalid > 0 ? nvalid - 1 : 0];
+  }
 
   // key-group shares: whole steps, group 0 first
   const int per = ((nvalid + C::KW * C::TR - 1) / (C::KW * C::TR)) * C::TR;

@@ -73,7 +73,10 @@ __device__ __forceinline__ float gldf(uint64_t a) { return *reinterpret_cast<con
 
 static __shared__ __attribute__((aligned(16))) uint4 lds_ring[kLdsRows * kChunksMax];  // 147,456 B
 // compacted rows of the workgroup: the byte address of each cache row
-static __shared__ uint64_t lds_rows[kMaxSlots];
+// (+ kRowPad entries past the compacted rows: copies of the last one, so a
+// streaming step's row lookups need no clamp)
+constexpr int kRowPad = 64;
+static __shared__ uint64_t lds_rows[kMaxSlots + kRowPad];
 static __shared__ int lds_cnt[kRoundsMax][kMaxWaves];
 static __shared__ float lds_ml[kMaxWaves][2][16];
 static __shared__ int lds_tok[2];   // resolve(): the token's batch and padded flag
