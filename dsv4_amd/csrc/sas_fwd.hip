@@ -173,9 +173,12 @@ struct Fwd {
     if constexpr (C::QL) {
       // lds_rows holds kRowPad copies of the last row past the compacted
       // ones, and a step's rows end within them: no clamp
-      const uint64_t* rows = lds_rows + rp;
+      // the step's first entry as one scalar LDS address, so each lookup
+      // is one add to the lane's constant offset
+      const uint32_t rb = __builtin_amdgcn_readfirstlane(lds_addr_of(lds_rows + rp));
 #pragma unroll
-      for (int o = 0; o < C::OPS; ++o) d.ra[o] = rows[drow(o)];
+      for (int o = 0; o < C::OPS; ++o)
+        d.ra[o] = *reinterpret_cast<const LDS_AS uint64_t*>((size_t)(rb + 8u * (uint32_t)drow(o)));
     } else {
       const int last = rp + min(C::TR, nrows - step * C::TR) - 1;   // nk >= 1 for every issued step
 #pragma unroll
@@ -444,17 +447,20 @@ struct Fwd {
   // and the reference max and l move by alpha = exp2(m_run - m_new) (1 when
   // no head rises past the lazy threshold). Returns whether O must be scaled
   // by alpha before the step's P.V (the caller does it after the MFMAs).
+  // kFull: the caller knows the step is full (every step but the last), so
+  // no key is masked.
+  template <bool kFull = false>
   __device__ __forceinline__ bool smax_front(const f32x4 (&sacc)[C::MT], int step, float (&sv)[C::MT][4],
                                              float& alpha) {
     constexpr int MT = C::MT;
-    const int nk = min(C::TR, nrows - step * C::TR);
+    const int nk = kFull ? C::TR : min(C::TR, nrows - step * C::TR);
     float mloc = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int key = mt * 16 + g * 4 + j;
-        const float x = key < nk ? sacc[mt][j] * p.scale_log2 : -INFINITY;
+        const float x = kFull || key < nk ? sacc[mt][j] * p.scale_log2 : -INFINITY;
         sv[mt][j] = x;
         mloc = fmaxf(mloc, x);
       }
@@ -860,7 +866,7 @@ struct Fwd {
       prep(d, Jf, it + 2);
       f32x4 sn[C::MT], so[C::MT];
       qk<true>(slot(Jn), sn, so, [&](int o) { fire(d, o); }, [&](int ks) {
-        if (ks == 0) resc = smax_front(sc, it, sv, alpha);
+        if (ks == 0) resc = smax_front<true>(sc, it, sv, alpha);   // step it < nsteps - 1: full
         else if (ks - 1 < kSmaxB) smax_b(ks - 1, sv, lsum, pk);
       });
 #pragma unroll
