@@ -427,6 +427,13 @@ def bench_backward(dec_inp, pre_inp, atomic_peak=None):
                         heads_per_workgroup=hpw, fp32_row_atomics=atomics, atomic_g_per_s=round(rate, 1),
                         atomic_frac=round(rate / atomic_peak, 3) if atomic_peak else None,
                         atomic_frac_of="peaks.fp32_atomic_measured_g_per_s")
+        if key == "prefill":
+            # the opt-in key-major window pass (window rows' gradients summed
+            # per row over their tokens), timed beside the default
+            del pb
+            pb = prepare_sparse_attn_sharedkv_backward(dout, inp.q, out, lse, window_pass=True, **kw)
+            ms, _ = time_launches(lambda i, st: pb.launch(st), 1, steps, 1)
+            res[key]["us_per_call_window_pass"] = round(ms * 1e3 / steps, 1)
         del pb, out, lse, dout
     return res
 

@@ -18,6 +18,8 @@ SAS_DT_BF16, SAS_DT_FP16, SAS_DT_FP8_E4M3_ROW656 = 0, 1, 2
 SAS_SWA, SAS_CFA, SAS_SCFA = 1, 2, 3
 SAS_META_SIZE = 1024
 SAS_FWD_NO_COMBINE = 1
+SAS_BWD_WINDOW_TOKENS = 2   # backward: per-token adds for window rows
+SAS_BWD_WINDOW_KEYS = 4     # backward: the key-major window pass
 
 EXPORTED = ("sas_metadata_v1", "sas_metadata_device_v1", "sas_fwd_plan", "sas_fwd_v1", "sas_fwd_noalloc_v1", "sas_combine_v1",
             "sas_cache_write_v1", "sas_bwd_v1", "sas_last_error", "sas_version",

@@ -752,8 +752,14 @@ class PreparedBackward:
 def prepare_sparse_attn_sharedkv_backward(dout: torch.Tensor, q: torch.Tensor, out: torch.Tensor,
                                           lse: torch.Tensor, **kwargs) -> PreparedBackward:
     """Validate and bind the arguments of :func:`sparse_attn_sharedkv_backward`
-    and allocate its (zeroed) gradient buffers."""
+    and allocate its (zeroed) gradient buffers. ``window_pass`` (keyword,
+    default None: the library's choice, per-token adds) selects how window
+    rows' gradients are summed: True, the key-major pass (each row's gradient
+    summed over the tokens whose window holds it, one add per 16 heads);
+    False, one add per (token, row); the results agree up to fp32 summation
+    order."""
     kwargs.pop("return_softmax_lse", None)
+    window_pass = kwargs.pop("window_pass", None)
     call = prepare_sparse_attn_sharedkv(q, **kwargs)
     # a copy: the forward's resolved split count stays with the forward. The
     # backward takes the caller's count, or plans its own (0); the forward's
@@ -761,6 +767,8 @@ def prepare_sparse_attn_sharedkv_backward(dout: torch.Tensor, q: torch.Tensor, o
     # CUs idle.
     a = _lib.SasFwdArgs.from_buffer_copy(call.args)
     a.num_splits = int(kwargs.get("num_splits", 0))
+    if window_pass is not None:
+        a.flags = _lib.SAS_BWD_WINDOW_KEYS if window_pass else _lib.SAS_BWD_WINDOW_TOKENS
     if a.kv_dtype != a.q_dtype:
         raise ValueError("the backward needs caches in the query dtype (fp8 rows are not differentiated)")
     T1, H = int(a.T), int(a.H)

@@ -51,6 +51,8 @@ struct BwdParams {
   float* d_ori;         // [ori rows, D] fp32, accumulated
   float* d_cmp;         // [cmp rows, D] fp32, accumulated (null for SWA)
   float* d_sinks;       // [H] fp32, accumulated
+  int win_pass;         // 1: window rows' gradients come from sas_bwd_win_kernel (the per-token kernels skip them)
+  int win_tiles;        // sas_bwd_win_kernel: 64-position row tiles per batch
 };
 
 // f(integral_constant<int, j>) for j = 0 .. N-1, with no loop: arrays
@@ -279,11 +281,13 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
       for (int i = 0; i < 4; ++i) {
         const int key = 4 * g4 + i;
         const uint64_t a = lds_rows[c0 + min(key, nr - 1)];
-        grow[i] = key < nr ? (a - ori_lo < ori_n ? bp.d_ori + (a - ori_lo) / (D * 2) * D
+        grow[i] = key < nr ? (a - ori_lo < ori_n ? (bp.win_pass ? nullptr : bp.d_ori + (a - ori_lo) / (D * 2) * D)
                                                  : bp.d_cmp + (a - cmp_lo) / (D * 2) * D)
                            : nullptr;
       }
-      for (int ct = wave; ct < D / 16; ct += 4 * NG) {
+      // a chunk of window rows only, under the window pass: no dkv here
+      const bool any_row = __ballot(grow[0] || grow[1] || grow[2] || grow[3]) != 0;
+      for (int ct = wave; any_row && ct < D / 16; ct += 4 * NG) {
         const int ch = ct * 16 + c16;
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -518,14 +522,16 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
       for (int i = 0; i < 4; ++i) {
         const int key = 4 * g4 + i;
         const uint64_t a = lds_rows[c0 + min(key, nr - 1)];
-        grow[i] = key < nr ? (a - ori_lo < ori_n ? bp.d_ori + (a - ori_lo) / (D * 2) * D
+        grow[i] = key < nr ? (a - ori_lo < ori_n ? (bp.win_pass ? nullptr : bp.d_ori + (a - ori_lo) / (D * 2) * D)
                                                  : bp.d_cmp + (a - cmp_lo) / (D * 2) * D)
                            : nullptr;
       }
+      // a chunk of window rows only, under the window pass: no dkv here
+      const bool any_row = __ballot(grow[0] || grow[1] || grow[2] || grow[3]) != 0;
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         const int ct = wave + 8 * m;
-        if (ct >= NCT) break;   // wave-uniform
+        if (ct >= NCT || !any_row) break;   // wave-uniform
         const int ch = ct * 16 + c16;
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -551,6 +557,267 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
       else atomicAdd(dqb + (size_t)i * D + ct * 16, dqt[j][i]);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// key-major pass over the window rows
+// ---------------------------------------------------------------------------
+//
+// A window row (position pos of batch b's raw cache) is a key of every token
+// of b whose window [max(s_g - win_left, 0), s_g] covers it: up to
+// win_left + 1 consecutive tokens of a prefill. The per-token kernels add one
+// fp32 atomic per (token, row, channel) for it; this pass instead keeps a
+// tile of 64 consecutive positions resident, streams the tokens that attend
+// any of them, and sums each row's gradient over those tokens in registers,
+// adding it once per 16-head group at the end (C3 prefill: 2.97e8 of the
+// 1.20e9 row atomics). Workgroup = (batch, 64-position tile, 16-head group),
+// 4 waves; wave w owns rows 16 w .. 16 w + 15 of the tile, their K^T
+// fragments in registers for the whole token loop, and their dkv^T
+// accumulators [576 channels x 16 rows]. Per token (q, dO and O of the 16
+// heads staged in LDS, double-buffered, the loads of the token two ahead in
+// flight in registers):
+//   S[head][row] = Q . K^T and dP = dO . V^T   (16x16x32 MFMA, A = q / dO
+//     rows from LDS, B = the wave's K^T registers; lane (g4, c16) holds
+//     heads 4 g4 .. + 3 of row c16)
+//   P = exp(scale S - lse), dS = P (dP - Delta) scale, masked to the
+//     token's window and valid rows, rounded to the query dtype
+//   dkv^T[ch][row] += Q^T[ch][head] . dS[head][row] (+ dO^T . P for the 512
+//     V channels)   (16x16x16 MFMA, A = a transposed read of the q / dO
+//     tile, B = dS / P exactly in the S accumulator's layout)
+// P, dS and their rounding are those of the per-token kernels, so the sum
+// differs from theirs only in fp32 summation order. Row validity follows
+// resolve(): position below act_kv, block inside the table, table entry
+// inside the cache. Runs only when the caller asks (SAS_BWD_WINDOW_KEYS):
+// measured slower overall on the C3 prefill (sas_bwd_v1).
+constexpr int kWinRows = 64;   // positions per tile (16 per wave)
+
+template <int D, typename QT>
+__global__ void __launch_bounds__(256) sas_bwd_win_kernel(const BwdParams bp) {
+  constexpr int HG = 16;                   // heads per workgroup
+  constexpr int CH = D / 8;                // 16-byte chunks per row
+  constexpr int KSN = D / 32;              // S k-steps
+  constexpr int VSN = kDV / 32;            // dP k-steps
+  constexpr int NCT = D / 16;              // dkv channel tiles
+  constexpr int RS = D * 2 + 16;           // row / q stride in LDS (bytes)
+  constexpr int OS = kDV * 2 + 16;         // dO stride in LDS (bytes)
+  constexpr int QL = (HG * CH + 255) / 256;   // q chunks per thread (16 threads per head)
+  constexpr int OL = kDV / 8 / 16;            // dO / O chunks per thread
+  static_assert(OL == 4 && HG * 16 == 256, "thread (head, part) layout");
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r[kWinRows * RS];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_tq[2][HG * RS];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_to[2][HG * OS];
+  __shared__ float lds_th[2][HG][2];       // per buffer and head: Delta, lse (log2 units)
+  __shared__ uint64_t lds_wr[kWinRows];    // row addresses (0: invalid row)
+
+  const FwdParams& p = bp.f;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int c16 = lane & 15, g4 = lane >> 4;
+  const int nhgw = p.H / HG;
+  const int hg = (int)(blockIdx.x % nhgw), rest = (int)(blockIdx.x / nhgw);
+  const int tile = rest % bp.win_tiles, b = rest / bp.win_tiles;
+  const int p0 = tile * kWinRows;
+  const bool cu = p.act_q == nullptr;
+  const int qp = p.q_prefix[b];
+  const int aq = cu ? p.q_prefix[b + 1] - qp : p.act_q[b];
+  const int akv = p.act_kv[b];
+  const int sg0 = akv - aq;                // causal position of the batch's first token
+  // tokens whose window meets [p0, p0 + 64): s_g in [p0, p0 + 63 + win_left]
+  // and in [max(sg0, 0), akv - 1]
+  const long long sg_lo = p0 > sg0 ? (p0 > 0 ? p0 : 0) : (sg0 > 0 ? sg0 : 0);
+  const long long sg_top = (long long)p0 + kWinRows - 1 + p.win_left;
+  long long sg_hi = sg_top < (long long)akv - 1 ? sg_top : (long long)akv - 1;
+  // (and tokens inside [0, T): lengths that point past the query tensor
+  // bring no token in)
+  const long long sg_tend = (long long)sg0 + (long long)p.T - 1 - qp;
+  if (sg_tend < sg_hi) sg_hi = sg_tend;
+  if (aq <= 0 || qp < 0 || qp >= p.T || sg_lo > sg_hi) return;   // uniform: no token of this tile
+  const int h0 = hg * HG;
+
+  // row tile: addresses (as resolve() validates them), then the rows
+  if (tid < kWinRows) {
+    const int pos = p0 + tid;
+    const int blk = pos / p.ori_bs;
+    uint64_t a = 0;
+    if (pos < akv && blk < p.ori_bt_stride) {
+      const int phys = p.ori_bt[(size_t)b * p.ori_bt_stride + blk];
+      if (phys >= 0 && phys < p.ori_nblocks)
+        a = reinterpret_cast<uint64_t>(p.ori_kv) + (uint64_t)((uint32_t)(phys * p.ori_bs + pos - blk * p.ori_bs)) * (D * 2);
+    }
+    lds_wr[tid] = a;
+  }
+  __syncthreads();
+  for (int i = tid; i < kWinRows * CH; i += 256) {
+    const int r = i / CH, c = i - r * CH;
+    const uint64_t a = lds_wr[r];
+    *reinterpret_cast<uint4*>(lds_r + r * RS + c * 16) = a ? gld16(a + c * 16) : make_uint4(0, 0, 0, 0);
+  }
+  __syncthreads();
+  // this wave's rows: K^T operands (row c16, channels 32 ks + 8 g4 ..) and
+  // the lane's row position / validity
+  uint4 kf[KSN];
+#pragma unroll
+  for (int ks = 0; ks < KSN; ++ks)
+    kf[ks] = *reinterpret_cast<const uint4*>(lds_r + (16 * wave + c16) * RS + (32 * ks + 8 * g4) * 2);
+  const int pos = p0 + 16 * wave + c16;
+  const bool rok = lds_wr[16 * wave + c16] != 0;
+  const int wpos0 = p0 + 16 * wave;        // the wave's first position
+
+  f32x4 acc[NCT];
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float scale = p.scale_log2 / kLog2e;
+
+  // Token staging: thread (head th = tid / 16, part tp = tid % 16) loads its
+  // share of a token's q, dO and O into one of two register sets, two tokens
+  // ahead of the token being computed (one token ahead left the global
+  // round trip exposed: 3 µs per token on the C3 prefill), and stores it
+  // into the LDS buffer of the same index, with the head's Delta = dO . O.
+  const int th = tid >> 4, tp = tid & 15;
+  uint4 rq[2][QL], rd[2][OL], ro[2][OL];
+  float rl[2] = {0.f, 0.f};
+  auto load_tok = [&](auto S, long long sg) __attribute__((always_inline)) {
+    constexpr int sl = decltype(S)::value;
+    const size_t t = (size_t)qp + (size_t)(sg - sg0);
+    const uint4* qg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.q) + (t * p.H + h0 + th) * D);
+    const uint4* dg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(bp.dout) + (t * p.H + h0 + th) * kDV);
+    const uint4* og = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(bp.out) + (t * p.H + h0 + th) * kDV);
+    unroll<QL>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const int c = tp + 16 * j;
+      rq[sl][j] = c < CH ? qg[c] : make_uint4(0, 0, 0, 0);
+    });
+    unroll<OL>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      rd[sl][j] = dg[tp * OL + j];
+      ro[sl][j] = og[tp * OL + j];
+    });
+    rl[sl] = p.lse[t * p.H + h0 + th];
+  };
+  auto store_tok = [&](auto S) __attribute__((always_inline)) {
+    constexpr int sl = decltype(S)::value;
+    unroll<QL>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const int c = tp + 16 * j;
+      if (c < CH) *reinterpret_cast<uint4*>(lds_tq[sl] + th * RS + c * 16) = rq[sl][j];
+    });
+    float dp = 0.f;
+    unroll<OL>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      *reinterpret_cast<uint4*>(lds_to[sl] + th * OS + (tp * OL + j) * 16) = rd[sl][j];
+      dp = dot2<QT>(rd[sl][j].x, ro[sl][j].x, dp);
+      dp = dot2<QT>(rd[sl][j].y, ro[sl][j].y, dp);
+      dp = dot2<QT>(rd[sl][j].z, ro[sl][j].z, dp);
+      dp = dot2<QT>(rd[sl][j].w, ro[sl][j].w, dp);
+    });
+    dp = sum16(dp);   // Delta of head th (its 16 lanes)
+    if (tp == 0) { lds_th[sl][th][0] = dp; lds_th[sl][th][1] = rl[sl] * kLog2e; }
+  };
+  // A operand: the 16-bit values of heads 4 g4 .. + 3 at channel 16 ct +
+  // c16, by one transposed read (rows padded by 16 bytes)
+  auto col4 = [&](const uint8_t* base, int stride, int ct) __attribute__((always_inline)) {
+    const uint8_t* a = base + (4 * g4 + (c16 >> 2)) * stride + (ct * 16 + 4 * (c16 & 3)) * 2;
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS i16x4*)(a)));
+  };
+  auto compute = [&](int buf, long long sg) __attribute__((always_inline)) {
+    const long long wlo = sg - p.win_left > 0 ? sg - p.win_left : 0;
+    if (wpos0 + 15 < wlo || wpos0 > sg) return;   // wave-uniform: none of my rows in this window
+    const uint8_t* tq = lds_tq[buf];
+    const uint8_t* to = lds_to[buf];
+    // With one wave per SIMD nothing else hides an LDS read's latency, so
+    // every operand read is issued kPfA (S, dP) or kPfC (dkv) MFMAs ahead
+    // of its use.
+    constexpr int kPfA = 4, kPfC = 8;
+    auto qfrag = [&](int ks) __attribute__((always_inline)) {
+      return *reinterpret_cast<const uint4*>(tq + c16 * RS + (32 * ks + 8 * g4) * 2);
+    };
+    auto ofrag = [&](int ks) __attribute__((always_inline)) {
+      return *reinterpret_cast<const uint4*>(to + c16 * OS + (32 * ks + 8 * g4) * 2);
+    };
+    // two accumulation chains each for S and dP (even / odd k-steps)
+    f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}}, dc[2] = {sc[0], sc[0]};
+    uint4 qa[kPfA], oa[kPfA];
+#pragma unroll
+    for (int i = 0; i < kPfA; ++i) { qa[i] = qfrag(i); oa[i] = ofrag(i); }
+#pragma unroll
+    for (int ks = 0; ks < KSN; ++ks) {
+      const uint4 a = qa[ks % kPfA];
+      if (ks + kPfA < KSN) qa[ks % kPfA] = qfrag(ks + kPfA);
+      sc[ks & 1] = mfma32k<QT>(a, kf[ks], sc[ks & 1]);
+      if (ks < VSN) {
+        const uint4 o = oa[ks % kPfA];
+        if (ks + kPfA < VSN) oa[ks % kPfA] = ofrag(ks + kPfA);
+        dc[ks & 1] = mfma32k<QT>(o, kf[ks], dc[ks & 1]);
+      }
+    }
+    const f32x4 s_ = sc[0] + sc[1], d_ = dc[0] + dc[1];
+    // lane (g4, c16): heads 4 g4 + i of row c16
+    const bool in = rok && pos >= wlo && pos <= sg;
+    float pr[4], ds[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * g4 + i;
+      pr[i] = in ? __builtin_amdgcn_exp2f(s_[i] * p.scale_log2 - lds_th[buf][h][1]) : 0.f;
+      ds[i] = pr[i] * (d_[i] - lds_th[buf][h][0]) * scale;
+    }
+    const uint2 b_p = make_uint2(pack2<QT>(pr[0], pr[1]), pack2<QT>(pr[2], pr[3]));
+    const uint2 b_ds = make_uint2(pack2<QT>(ds[0], ds[1]), pack2<QT>(ds[2], ds[3]));
+    // dkv: every tile's dS MFMA, then every V tile's P MFMA (a tile's two
+    // adds 36 MFMAs apart instead of back to back)
+    uint2 cq[kPfC];
+#pragma unroll
+    for (int i = 0; i < kPfC; ++i) cq[i] = col4(tq, RS, i);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const uint2 a = cq[ct % kPfC];
+      cq[ct % kPfC] = ct + kPfC < NCT ? col4(tq, RS, ct + kPfC) : col4(to, OS, ct + kPfC - NCT);
+      acc[ct] = mfma16k<QT>(a, b_ds, acc[ct]);
+    }
+#pragma unroll
+    for (int ct = 0; ct < kDV / 16; ++ct) {
+      const uint2 o = cq[(NCT + ct) % kPfC];
+      if (ct + kPfC < kDV / 16) cq[(NCT + ct) % kPfC] = col4(to, OS, ct + kPfC);
+      acc[ct] = mfma16k<QT>(o, b_p, acc[ct]);
+    }
+  };
+  // one token from register set / LDS buffer S: store it, start the loads
+  // of the token two ahead into the freed registers, then (after the
+  // barrier, by which every wave has left the compute that last read
+  // buffer S) compute it. The loads go out unconditionally (past
+  // the last token they re-read it), and the barrier waits for the LDS
+  // stores only:
+  // a conditional load, or a barrier that also drains the loads in flight
+  // (__syncthreads), made every token wait for the next one's loads.
+  const std::integral_constant<int, 0> S0;
+  const std::integral_constant<int, 1> S1;
+  auto step = [&](auto S, long long sg, long long sg_next2) __attribute__((always_inline)) {
+    store_tok(S);
+    load_tok(S, sg_next2);
+    lds_barrier();
+    compute(decltype(S)::value, sg);
+  };
+  load_tok(S0, sg_lo);
+  load_tok(S1, sg_lo + 1 <= sg_hi ? sg_lo + 1 : sg_hi);
+  for (long long sg = sg_lo; sg <= sg_hi; sg += 2) {
+    step(S0, sg, sg + 2 <= sg_hi ? sg + 2 : sg_hi);
+    if (sg + 1 <= sg_hi) step(S1, sg + 1, sg + 3 <= sg_hi ? sg + 3 : sg_hi);   // uniform
+  }
+  // lane (g4, c16): channels 16 ct + 4 g4 .. + 3 of row c16
+  if (rok) {
+    const uint64_t a = lds_wr[16 * wave + c16];
+    float* gr = bp.d_ori + (a - reinterpret_cast<uint64_t>(p.ori_kv)) / (D * 2) * D + 4 * g4;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) atomicAdd(gr + ct * 16 + i, acc[ct][i]);
+  }
+}
+
+template <int D, typename QT>
+int launch_bwd_win(const BwdParams& bp, int nblocks, hipStream_t st) {
+  hipLaunchKernelGGL((sas_bwd_win_kernel<D, QT>), dim3(nblocks), dim3(256), 0, st, bp);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(SAS_ELAUNCH, "sas_bwd_win launch: %s", hipGetErrorString(e));
+  return SAS_OK;
 }
 
 template <int D, typename QT>
@@ -671,15 +938,44 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   const long long nblocks_ll = (long long)((a->T + kXcds - 1) / kXcds) * fp.nhg * fp.nsplit * kXcds;
   if (nblocks_ll > INT_MAX) return set_error(SAS_EINVAL, "bwd: %lld workgroups beyond one launch", nblocks_ll);
   const int nblocks = (int)nblocks_ll;
+  // The key-major window pass (sas_bwd_win_kernel) only when asked. On the
+  // C3 prefill it takes the window rows' 2.97e8 atomics out of the per-token
+  // kernel (3.97 -> 3.46 ms) but costs 575 µs itself (each token's q / dO / O
+  // streamed by ~3 tiles: ~200 µs of loads; ~310 µs of MFMA and LDS work
+  // with one wave per SIMD; ~180 µs per-token staging and barriers): 4.03
+  // against 3.97 ms. Its grid covers every position a block table can
+  // address, so decode-like calls (one token per batch, no shared rows)
+  // gain nothing from it either.
+  if ((a->flags & SAS_BWD_WINDOW_TOKENS) && (a->flags & SAS_BWD_WINDOW_KEYS))
+    return set_error(SAS_EINVAL, "bwd: SAS_BWD_WINDOW_TOKENS and SAS_BWD_WINDOW_KEYS together");
+  const bool win = (a->flags & SAS_BWD_WINDOW_KEYS) != 0;
+  long long win_blocks = 0;
+  if (win) {
+    const long long tiles = ((long long)a->ori_bt_stride * a->ori_block_size + kWinRows - 1) / kWinRows;
+    win_blocks = (long long)a->B * tiles * (a->H / 16);
+    if (tiles > INT_MAX || win_blocks > INT_MAX)
+      return set_error(SAS_EINVAL, "bwd: %lld window-pass workgroups beyond one launch", win_blocks);
+    bp.win_pass = 1;
+    bp.win_tiles = (int)tiles;
+  }
   hipStream_t st = (hipStream_t)stream;
+  int rc;
   if (b64) {
     if (a->q_dtype == SAS_DT_BF16)
-      return a->D == 576 ? launch_bwd64<576, __bf16>(bp, nblocks, st) : launch_bwd64<512, __bf16>(bp, nblocks, st);
-    return a->D == 576 ? launch_bwd64<576, _Float16>(bp, nblocks, st) : launch_bwd64<512, _Float16>(bp, nblocks, st);
-  }
-  if (a->q_dtype == SAS_DT_BF16)
-    return a->D == 576 ? launch_bwd_ng<576, __bf16>(bp, ng, nblocks, st)
-                       : launch_bwd_ng<512, __bf16>(bp, ng, nblocks, st);
-  return a->D == 576 ? launch_bwd_ng<576, _Float16>(bp, ng, nblocks, st)
+      rc = a->D == 576 ? launch_bwd64<576, __bf16>(bp, nblocks, st) : launch_bwd64<512, __bf16>(bp, nblocks, st);
+    else
+      rc = a->D == 576 ? launch_bwd64<576, _Float16>(bp, nblocks, st) : launch_bwd64<512, _Float16>(bp, nblocks, st);
+  } else if (a->q_dtype == SAS_DT_BF16) {
+    rc = a->D == 576 ? launch_bwd_ng<576, __bf16>(bp, ng, nblocks, st)
+                     : launch_bwd_ng<512, __bf16>(bp, ng, nblocks, st);
+  } else {
+    rc = a->D == 576 ? launch_bwd_ng<576, _Float16>(bp, ng, nblocks, st)
                      : launch_bwd_ng<512, _Float16>(bp, ng, nblocks, st);
+  }
+  if (rc || !win || win_blocks == 0) return rc;
+  if (a->q_dtype == SAS_DT_BF16)
+    return a->D == 576 ? launch_bwd_win<576, __bf16>(bp, (int)win_blocks, st)
+                       : launch_bwd_win<512, __bf16>(bp, (int)win_blocks, st);
+  return a->D == 576 ? launch_bwd_win<576, _Float16>(bp, (int)win_blocks, st)
+                     : launch_bwd_win<512, _Float16>(bp, (int)win_blocks, st);
 }

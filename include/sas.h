@@ -152,6 +152,17 @@ typedef struct SasFwdArgs {
    sas_combine_v1 itself, e.g. to time or overlap the two kernels apart. */
 #define SAS_FWD_NO_COMBINE 1
 
+/* SasFwdArgs.flags of a sas_bwd_v1 call (the forward rejects them): how the
+   window rows' gradients are summed. By default (and with
+   SAS_BWD_WINDOW_TOKENS) one fp32 add per (token, row, head group, channel);
+   with SAS_BWD_WINDOW_KEYS a key-major pass instead sums each window row's
+   gradient over the tokens whose window holds it and adds it once per
+   16-head group (a second kernel; the same result up to fp32 summation
+   order, slower on the measured prefill, kept for callers whose atomics are
+   scarcer). */
+#define SAS_BWD_WINDOW_TOKENS 2   /* per-token adds for window rows (the default) */
+#define SAS_BWD_WINDOW_KEYS 4     /* the key-major window pass */
+
 /*
  * Split count the library would use (after auto-selection) and the
  * workspace bytes it needs for these arguments (0 when no split is used).
@@ -222,7 +233,9 @@ int sas_combine_v1(const SasCombineArgs* a, void* stream);
  * All four outputs must be zeroed by the caller first; cache rows (and dq
  * with several KV splits) receive atomic fp32 adds, so their summation order
  * varies. Tokens with more than 1280 key slots (win_left + 1 + K) are split
- * across several workgroups.
+ * across several workgroups. fwd.flags may hold SAS_BWD_WINDOW_TOKENS or
+ * SAS_BWD_WINDOW_KEYS (how the window rows' gradients are summed; same
+ * result up to fp32 summation order).
  */
 typedef struct SasBwdArgs {
   SasFwdArgs fwd;

@@ -299,6 +299,73 @@ def test_gpu_backward_c3_prefill_sampled():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("name", ["prefill_2b", "prefill_bs16_h16", "swa", "short_kv", "decode_h64", "cfa",
+                                  "fp16_d512", "prefill_wide_window", "prefill_swa_bs16"])
+def test_gpu_backward_window_pass_both_ways(name):
+    """Window rows' gradients summed per (token, row) and by the key-major
+    window pass (forced both ways, whatever the library would choose): each
+    element-wise against the fp64 oracle, on prefills (several batches, BSND
+    pages of 16, a window wider than the 64-position tile) and on
+    decode and short-KV batches (tokens with empty windows, rows past
+    act_kv)."""
+    from dsv4_amd.api import sparse_attn_sharedkv, sparse_attn_sharedkv_backward
+    from tests.test_gpu_parity import _small
+    extra = {
+        "prefill_2b": dict(B=2, H=64, q_lens=[300, 170], kv_lens=[300, 420], K=64, bs=64),
+        "prefill_bs16_h16": dict(B=3, H=16, q_lens=[90, 17, 64], kv_lens=[90, 200, 64], K=32, bs=16),
+        "prefill_wide_window": dict(B=1, H=32, q_lens=[400], kv_lens=[400], K=48, win=300),
+        "prefill_swa_bs16": dict(B=2, H=16, q_lens=[200, 70], kv_lens=[260, 70], K=0, scenario=1, bs=16),
+    }
+    inp = _small(**extra[name]) if name in extra else _gpu_case(name)
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    out, lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+    g = torch.Generator().manual_seed(31)
+    dout = torch.randn(out.shape, generator=g).to(inp.q.dtype)
+    r = _oracle_bwd(inp, dout, out, lse)
+    for wp in (False, True):
+        dq, d_ori, d_cmp, d_sinks = sparse_attn_sharedkv_backward(dout.cuda(), d.q, out, lse, window_pass=wp, **kw)
+        torch.cuda.synchronize()
+        _check_against_oracle(f"{name} window_pass={wp}", inp, dq, d_ori, d_cmp, d_sinks, r)
+
+
+@pytest.mark.gpu
+def test_gpu_backward_window_pass_bsnd():
+    """The key-major window pass with BSND queries (per-batch lengths, padded
+    rows: the kernel reads act_q instead of a prefix difference) gives the
+    TND per-token result up to summation order."""
+    from tests.test_gpu_parity import _small
+    from dsv4_amd.api import sparse_attn_sharedkv, sparse_attn_sharedkv_backward
+    q_lens = [70, 30]
+    inp = _small(B=2, H=64, q_lens=q_lens, kv_lens=[90, 30], K=16)
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    out, lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+    g = torch.Generator().manual_seed(33)
+    dout = torch.randn(out.shape, generator=g).to(out.dtype).cuda()
+    ref = sparse_attn_sharedkv_backward(dout, d.q, out, lse, window_pass=False, **kw)
+    S = max(q_lens)
+    q_b = torch.zeros(2, S, 64, 576, dtype=torch.bfloat16, device="cuda")
+    idx_b = torch.full((2, S, 1, 16), -1, dtype=torch.int32, device="cuda")
+    o_b = torch.zeros(2, S, 64, 512, dtype=torch.bfloat16, device="cuda")
+    l_b = torch.zeros(2, S, 64, dtype=torch.float32, device="cuda")
+    do_b = torch.zeros(2, S, 64, 512, dtype=torch.bfloat16, device="cuda")
+    t_ = 0
+    for b, n in enumerate(q_lens):
+        q_b[b, :n], idx_b[b, :n], o_b[b, :n], l_b[b, :n], do_b[b, :n] = (
+            d.q[t_:t_ + n], d.cmp_idx[t_:t_ + n], out[t_:t_ + n], lse[t_:t_ + n], dout[t_:t_ + n])
+        t_ += n
+    kwb = dict(kw, layout_q="BSND", cmp_sparse_indices=idx_b)
+    dq_b, d_ori, d_cmp, d_snk = sparse_attn_sharedkv_backward(do_b, q_b, o_b, l_b, window_pass=True, **kwb)
+    torch.cuda.synchronize()
+    assert _rel_err(dq_b[0, :70].float().cpu(), ref[0][:70].float().cpu()) < 1e-2
+    assert _rel_err(dq_b[1, :30].float().cpu(), ref[0][70:].float().cpu()) < 1e-2
+    assert torch.count_nonzero(dq_b[1, 30:].cpu().float()) == 0
+    assert _rel_err(d_ori.cpu(), ref[1].cpu()) < 1e-4 and _rel_err(d_cmp.cpu(), ref[2].cpu()) < 1e-4
+    assert _rel_err(d_snk.cpu(), ref[3].cpu()) < 1e-4
+
+
+@pytest.mark.gpu
 def test_gpu_backward_split_count_invariance():
     """The key range split over 1, 3 or 7 workgroups per (token, head group)
     (dq then accumulated atomically) gives the same gradients up to fp32
