@@ -28,7 +28,7 @@ def test_header_declares_the_exported_set():
 
 def test_python_constants_match_the_header():
     text = open(HEADER).read()
-    for name in ("SAS_FWD_NO_COMBINE", "SAS_META_SIZE"):
+    for name in ("SAS_FWD_NO_COMBINE", "SAS_META_SIZE", "SAS_BWD_WINDOW_TOKENS", "SAS_BWD_WINDOW_KEYS"):
         m = re.search(r"^#define\s+%s\s+(\d+)" % name, text, flags=re.M)
         assert m and int(m.group(1)) == getattr(_lib, name), name
 
@@ -153,3 +153,20 @@ def test_plan_long_rows_take_more_than_64_splits():
     assert rc == _lib.SAS_OK and ns >= 1
     rc, _, _ = _plan(_valid_args(scenario=_lib.SAS_CFA, K=(1 << 16) * 1280))
     assert rc == _lib.SAS_EINVAL
+
+
+def test_bwd_rejects_both_window_modes_and_fwd_rejects_bwd_flags():
+    """sas_bwd_v1 takes one of the two window-gradient modes, never both
+    (refused before any device work); the forward refuses the backward's
+    flags."""
+    fake = 1 << 40  # never dereferenced: validation fails first
+    a = _valid_args(flags=_lib.SAS_BWD_WINDOW_TOKENS | _lib.SAS_BWD_WINDOW_KEYS)
+    for f in ("q", "ori_kv", "ori_block_table", "cmp_kv", "cmp_block_table", "cmp_indices",
+              "q_prefix", "act_q", "act_kv", "sinks", "out", "lse"):
+        setattr(a, f, fake)
+    ba = _lib.SasBwdArgs(fwd=a, dout=fake, dq=fake, d_ori_kv=fake, d_cmp_kv=fake, d_sinks=fake)
+    assert _lib.lib().sas_bwd_v1(C.byref(ba), None) == _lib.SAS_EINVAL
+    assert "together" in _lib.lib().sas_last_error().decode()
+    for fl in (_lib.SAS_BWD_WINDOW_TOKENS, _lib.SAS_BWD_WINDOW_KEYS):
+        rc, _, _ = _plan(_valid_args(flags=fl))
+        assert rc == _lib.SAS_EINVAL and "flags" in _lib.lib().sas_last_error().decode()
