@@ -403,7 +403,8 @@ def bench_backward(dec_inp, pre_inp, atomic_peak=None):
     from dsv4_amd import cases
     from dsv4_amd.api import prepare_sparse_attn_sharedkv_backward, sparse_attn_sharedkv
     res = {"kernel": "sas_bwd64_kernel (64-head workgroups, q in registers; MFMA scores, dq and dkv; "
-                     "fp32 atomics for dkv); sas_bwd_kernel for H not a multiple of 64",
+                     "fp32 atomics for dkv); sas_bwd_kernel for H not a multiple of 64; prefills: the "
+                     "window rows' dkv by sas_bwd_win_kernel beside it on a side stream",
            "flop_per_pair_head": BWD_FLOP_PER_PAIR_HEAD}
     for key, inp, steps in (("decode", dec_inp, 50), ("prefill", pre_inp, 3)):
         if inp is None:
@@ -420,20 +421,31 @@ def bench_backward(dec_inp, pre_inp, atomic_peak=None):
         tfl = flop / (us * 1e-6) / 1e12
         hpw = 64 if inp.cfg.H % 64 == 0 else 32 if inp.cfg.H % 32 == 0 else 16
         D = inp.q.shape[-1]
+        # the library's default: the key-major window pass for prefills (at
+        # least 64 query tokens per batch), whose window rows take one add
+        # per (row, 16-head group, channel) instead of one per (token, row)
+        win_pass = inp.q.shape[0] >= 64 * len(inp.q_lens)
+        win_pairs, win_rows = 0, 0
+        for aq, akv in zip(inp.q_lens, inp.kv_lens):
+            wl = inp.cfg.win_left
+            win_pairs += sum(min(akv - aq + s, wl) + 1 for s in range(aq) if akv - aq + s >= 0)
+            win_rows += akv - max(akv - aq - wl, 0) if aq > 0 else 0
         atomics = pairs * (inp.cfg.H // hpw) * D
+        if win_pass:
+            atomics = ((pairs - win_pairs) * (inp.cfg.H // hpw) + win_rows * (inp.cfg.H // 16)) * D
         rate = atomics / (us * 1e-6) / 1e9
         res[key] = dict(workload=inp.cfg.name, us_per_call=round(us, 1), useful_flop=flop,
                         tflops=round(tfl, 2), mfma_frac=round(tfl / BF16_PEAK_TFLOPS, 5),
-                        heads_per_workgroup=hpw, fp32_row_atomics=atomics, atomic_g_per_s=round(rate, 1),
+                        heads_per_workgroup=hpw, window_pass=win_pass, fp32_row_atomics=atomics,
+                        atomic_g_per_s=round(rate, 1),
                         atomic_frac=round(rate / atomic_peak, 3) if atomic_peak else None,
                         atomic_frac_of="peaks.fp32_atomic_measured_g_per_s")
-        if key == "prefill":
-            # the opt-in key-major window pass (window rows' gradients summed
-            # per row over their tokens), timed beside the default
+        if win_pass:
+            # the same launch with per-token adds for the window rows too
             del pb
-            pb = prepare_sparse_attn_sharedkv_backward(dout, inp.q, out, lse, window_pass=True, **kw)
+            pb = prepare_sparse_attn_sharedkv_backward(dout, inp.q, out, lse, window_pass=False, **kw)
             ms, _ = time_launches(lambda i, st: pb.launch(st), 1, steps, 1)
-            res[key]["us_per_call_window_pass"] = round(ms * 1e3 / steps, 1)
+            res[key]["us_per_call_per_token_adds"] = round(ms * 1e3 / steps, 1)
         del pb, out, lse, dout
     return res
 

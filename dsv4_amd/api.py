@@ -753,10 +753,11 @@ def prepare_sparse_attn_sharedkv_backward(dout: torch.Tensor, q: torch.Tensor, o
                                           lse: torch.Tensor, **kwargs) -> PreparedBackward:
     """Validate and bind the arguments of :func:`sparse_attn_sharedkv_backward`
     and allocate its (zeroed) gradient buffers. ``window_pass`` (keyword,
-    default None: the library's choice, per-token adds) selects how window
-    rows' gradients are summed: True, the key-major pass (each row's gradient
-    summed over the tokens whose window holds it, one add per 16 heads);
-    False, one add per (token, row); the results agree up to fp32 summation
+    default None: the library's choice, the key-major pass for prefills)
+    selects how window rows' gradients are summed: True, the key-major pass
+    (each row's gradient summed over the tokens whose window holds it, one
+    add per 16 heads, beside the per-token kernel on a side stream); False,
+    one add per (token, row); the results agree up to fp32 summation
     order."""
     kwargs.pop("return_softmax_lse", None)
     window_pass = kwargs.pop("window_pass", None)

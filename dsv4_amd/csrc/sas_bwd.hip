@@ -27,6 +27,7 @@
 // over the heads, added to the fp32 gradient cache rows with atomics) are
 // 16x16x16 MFMAs per 16-channel tile.
 
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -587,8 +588,8 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
 // P, dS and their rounding are those of the per-token kernels, so the sum
 // differs from theirs only in fp32 summation order. Row validity follows
 // resolve(): position below act_kv, block inside the table, table entry
-// inside the cache. Runs only when the caller asks (SAS_BWD_WINDOW_KEYS):
-// measured slower overall on the C3 prefill (sas_bwd_v1).
+// inside the cache. It runs beside the per-token kernel on a side stream
+// (SideStream below); sas_bwd_v1 chooses it for prefills.
 constexpr int kWinRows = 64;   // positions per tile (16 per wave)
 
 template <int D, typename QT>
@@ -820,6 +821,41 @@ int launch_bwd_win(const BwdParams& bp, int nblocks, hipStream_t st) {
   return SAS_OK;
 }
 
+// The window pass runs beside the per-token kernel, on a side stream of the
+// library's (one per device, created on first use, default priority; forked
+// from and joined back to the caller's stream by events): the per-token
+// kernel is bound by the device's fp32 atomic rate, which 128 of the 256 CUs
+// already reach (sas_bench_atomic_add_v1 with 128 four-wave workgroups:
+// 323 G adds/s, with 2048: 326), so the window pass's workgroups take CUs it
+// does not need. The two kernels write disjoint outputs (the per-token
+// kernel skips the window rows' gradients). Calls made under stream capture
+// run the two kernels one after the other on the caller's stream.
+struct SideStream {
+  hipStream_t st = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mu;
+SideStream g_side[64];
+
+int side_stream(SideStream** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return set_error(SAS_ELAUNCH, "bwd: no device for the window pass's side stream");
+  }
+  SideStream& s = g_side[dev];
+  if (!s.st) {
+    if (hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess) {
+      const hipError_t e = hipGetLastError();
+      return set_error(SAS_ELAUNCH, "bwd: side stream: %s", hipGetErrorString(e));
+    }
+  }
+  *out = &s;
+  return SAS_OK;
+}
+
 template <int D, typename QT>
 int launch_bwd64(const BwdParams& bp, int nblocks, hipStream_t st) {
   hipLaunchKernelGGL((sas_bwd64_kernel<D, QT>), dim3(nblocks), dim3(512), 0, st, bp);
@@ -938,17 +974,30 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   const long long nblocks_ll = (long long)((a->T + kXcds - 1) / kXcds) * fp.nhg * fp.nsplit * kXcds;
   if (nblocks_ll > INT_MAX) return set_error(SAS_EINVAL, "bwd: %lld workgroups beyond one launch", nblocks_ll);
   const int nblocks = (int)nblocks_ll;
-  // The key-major window pass (sas_bwd_win_kernel) only when asked. On the
-  // C3 prefill it takes the window rows' 2.97e8 atomics out of the per-token
-  // kernel (3.97 -> 3.46 ms) but costs 575 µs itself (each token's q / dO / O
-  // streamed by ~3 tiles: ~200 µs of loads; ~310 µs of MFMA and LDS work
-  // with one wave per SIMD; ~180 µs per-token staging and barriers): 4.03
-  // against 3.97 ms. Its grid covers every position a block table can
-  // address, so decode-like calls (one token per batch, no shared rows)
-  // gain nothing from it either.
+  // The key-major window pass (sas_bwd_win_kernel): by default when query
+  // tokens share window rows (at least 64 query tokens per batch on
+  // average, a prefill) and the call is not being captured, else when asked.
+  // On the C3 prefill it takes the window rows' 2.97e8 atomics out of the
+  // per-token kernel (3.97 -> 3.46 ms) and costs 575 µs itself (each token's
+  // q / dO / O streamed by ~3 tiles: ~200 µs of loads; ~310 µs of MFMA and
+  // LDS work with one wave per SIMD; ~180 µs per-token staging and
+  // barriers); run after it, 4.03 against 3.97 ms, run beside it on the side
+  // stream, 3.70 ms. Decode-like calls (one token per batch) share no rows,
+  // and the pass's grid covers every position a block table can address:
+  // per-token adds there.
   if ((a->flags & SAS_BWD_WINDOW_TOKENS) && (a->flags & SAS_BWD_WINDOW_KEYS))
     return set_error(SAS_EINVAL, "bwd: SAS_BWD_WINDOW_TOKENS and SAS_BWD_WINDOW_KEYS together");
-  const bool win = (a->flags & SAS_BWD_WINDOW_KEYS) != 0;
+  bool capturing = false;
+  {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) {
+      (void)hipGetLastError();
+      cs = hipStreamCaptureStatusActive;   // unknown: as if capturing
+    }
+    capturing = cs != hipStreamCaptureStatusNone;
+  }
+  const bool win = (a->flags & SAS_BWD_WINDOW_KEYS) ||
+                   (!(a->flags & SAS_BWD_WINDOW_TOKENS) && !capturing && a->T >= 64 * a->B);
   long long win_blocks = 0;
   if (win) {
     const long long tiles = ((long long)a->ori_bt_stride * a->ori_block_size + kWinRows - 1) / kWinRows;
@@ -959,6 +1008,22 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
     bp.win_tiles = (int)tiles;
   }
   hipStream_t st = (hipStream_t)stream;
+  // window pass beside the per-token kernel (see SideStream)
+  std::unique_lock<std::mutex> side_lock(g_side_mu, std::defer_lock);
+  SideStream* side = nullptr;
+  if (win && win_blocks > 0) {
+    if (!capturing) {
+      side_lock.lock();
+      const int src = side_stream(&side);
+      if (src) return src;
+      // fork: the side stream starts after everything the caller queued
+      // before this call (the inputs), not after the per-token kernel
+      if (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->st, side->fork, 0) != hipSuccess) {
+        const hipError_t e = hipGetLastError();
+        return set_error(SAS_ELAUNCH, "bwd: fork to the side stream: %s", hipGetErrorString(e));
+      }
+    }
+  }
   int rc;
   if (b64) {
     if (a->q_dtype == SAS_DT_BF16)
@@ -973,9 +1038,19 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
                      : launch_bwd_ng<512, _Float16>(bp, ng, nblocks, st);
   }
   if (rc || !win || win_blocks == 0) return rc;
+  hipStream_t wst = side ? side->st : st;
   if (a->q_dtype == SAS_DT_BF16)
-    return a->D == 576 ? launch_bwd_win<576, __bf16>(bp, (int)win_blocks, st)
-                       : launch_bwd_win<512, __bf16>(bp, (int)win_blocks, st);
-  return a->D == 576 ? launch_bwd_win<576, _Float16>(bp, (int)win_blocks, st)
-                     : launch_bwd_win<512, _Float16>(bp, (int)win_blocks, st);
+    rc = a->D == 576 ? launch_bwd_win<576, __bf16>(bp, (int)win_blocks, wst)
+                     : launch_bwd_win<512, __bf16>(bp, (int)win_blocks, wst);
+  else
+    rc = a->D == 576 ? launch_bwd_win<576, _Float16>(bp, (int)win_blocks, wst)
+                     : launch_bwd_win<512, _Float16>(bp, (int)win_blocks, wst);
+  if (side) {
+    // join: the caller's stream continues once the window pass is done
+    if (hipEventRecord(side->join, side->st) != hipSuccess || hipStreamWaitEvent(st, side->join, 0) != hipSuccess) {
+      const hipError_t e = hipGetLastError();
+      return set_error(SAS_ELAUNCH, "bwd: join from the side stream: %s", hipGetErrorString(e));
+    }
+  }
+  return rc;
 }

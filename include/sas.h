@@ -153,14 +153,17 @@ typedef struct SasFwdArgs {
 #define SAS_FWD_NO_COMBINE 1
 
 /* SasFwdArgs.flags of a sas_bwd_v1 call (the forward rejects them): how the
-   window rows' gradients are summed. By default (and with
-   SAS_BWD_WINDOW_TOKENS) one fp32 add per (token, row, head group, channel);
-   with SAS_BWD_WINDOW_KEYS a key-major pass instead sums each window row's
-   gradient over the tokens whose window holds it and adds it once per
-   16-head group (a second kernel; the same result up to fp32 summation
-   order, slower on the measured prefill, kept for callers whose atomics are
-   scarcer). */
-#define SAS_BWD_WINDOW_TOKENS 2   /* per-token adds for window rows (the default) */
+   window rows' gradients are summed. SAS_BWD_WINDOW_TOKENS: one fp32 add per
+   (token, row, head group, channel). SAS_BWD_WINDOW_KEYS: a key-major pass
+   sums each window row's gradient over the tokens whose window holds it and
+   adds it once per 16-head group; it runs beside the per-token kernel on a
+   side stream of the library (one per device, created on first use, forked
+   from and joined back to `stream` by events; one after the other on
+   `stream` while it is being captured). Neither flag: the key-major pass for
+   calls with at least 64 query tokens per batch on average that are not
+   being captured, per-token adds otherwise. The results agree up to fp32
+   summation order. */
+#define SAS_BWD_WINDOW_TOKENS 2   /* per-token adds for window rows */
 #define SAS_BWD_WINDOW_KEYS 4     /* the key-major window pass */
 
 /*

@@ -366,6 +366,52 @@ def test_gpu_backward_window_pass_bsnd():
 
 
 @pytest.mark.gpu
+def test_gpu_backward_captured_in_a_graph():
+    """The backward of a prefill captured in a HIP graph: eagerly the window
+    pass runs beside the per-token kernel on the library's side stream;
+    under capture it either gives way to per-token adds (the default) or,
+    when asked for, runs after the per-token kernel on the captured stream.
+    Every replay (with eager work between them) equals the eager run of the
+    same mode up to fp32 summation order; the two modes differ from each
+    other only by where the window keys' products are rounded."""
+    from dsv4_amd.api import prepare_sparse_attn_sharedkv_backward, sparse_attn_sharedkv
+    from tests.test_gpu_parity import _small
+    inp = _small(B=2, H=64, q_lens=[300, 170], kv_lens=[300, 420], K=64)
+    d = inp.to("cuda")
+    kw = d.api_kwargs()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out, lse = sparse_attn_sharedkv(d.q, return_softmax_lse=True, **kw)
+        g = torch.Generator().manual_seed(35)
+        dout = torch.randn(out.shape, generator=g).to(out.dtype).cuda()
+        refs = {}
+        for wp in (False, True):
+            eager = prepare_sparse_attn_sharedkv_backward(dout, d.q, out, lse, window_pass=wp, **kw)
+            eager.launch(side)
+            torch.cuda.synchronize()
+            refs[wp] = [t.clone() for t in (eager.dq, eager.d_ori_kv, eager.d_cmp_kv, eager.d_sinks)]
+        for a, b in zip(refs[False], refs[True]):
+            assert _rel_err(a.cpu(), b.cpu()) < 1e-4
+        for wp, mode in ((None, False), (True, True)):
+            pb = prepare_sparse_attn_sharedkv_backward(dout, d.q, out, lse, window_pass=wp, **kw)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=side):
+                pb.zero_grads()
+                pb.launch(side)
+            grads = (pb.dq, pb.d_ori_kv, pb.d_cmp_kv, pb.d_sinks)
+            for i in range(3):
+                for t in grads:
+                    t.fill_(float(i + 7))             # eager work between replays
+                graph.replay()
+                torch.cuda.synchronize()
+                for name, got, want in zip(("dq", "d_ori", "d_cmp", "d_sinks"), grads, refs[mode]):
+                    assert _rel_err(got.cpu(), want.cpu()) < 1e-5, f"window_pass={wp} replay {i} {name}"
+            del graph, pb
+
+
+@pytest.mark.gpu
 def test_gpu_backward_split_count_invariance():
     """The key range split over 1, 3 or 7 workgroups per (token, head group)
     (dq then accumulated atomically) gives the same gradients up to fp32
