@@ -43,6 +43,15 @@
 #ifndef SAS_KG2_SPLIT_MERGE
 #define SAS_KG2_SPLIT_MERGE 1   // two key-groups each merge and store half the channels
 #endif
+#ifndef SAS_F8_PFK
+#define SAS_F8_PFK 2   // fp8-resident: K fragments read ahead
+#endif
+#ifndef SAS_F8_PFV
+#define SAS_F8_PFV 2   // fp8-resident: V^T fragments read ahead
+#endif
+#ifndef SAS_FP8_RESIDENT
+#define SAS_FP8_RESIDENT 2   // fp8 mode of the 32-head 8-wave plan (1: rows converted into bf16 slots)
+#endif
 #ifndef SAS_PFV
 #define SAS_PFV 4   // V^T operand channel tiles read ahead (32-row steps)
 #endif
@@ -62,6 +71,12 @@ namespace {
 // both halves compute the same S = QK^T, each accumulates its own channels.
 template <int HW, int NW, int D, typename QT, int KVF>
 struct Cfg {
+  // KVF == 2: fp8 rows stay fp8 in LDS (LDS-DMA like bf16 rows) and each
+  // operand fragment is converted to bf16 in registers just before its
+  // MFMA; a 656-byte slot row lets two key-groups hold three 32-row slots
+  // each. (KVF == 1: rows are converted once, through registers, into bf16
+  // slots of 16 rows.)
+  static constexpr bool F8R = KVF == 2;
   static constexpr int CS = NW == 8 ? 2 : 1;
   static constexpr int WK = HW * CS;                        // waves sharing a key-group's slots
   static constexpr int KW = NW / WK;
@@ -73,9 +88,9 @@ struct Cfg {
   static constexpr bool QS = CS == 2;
   static constexpr int kRingRows = QS ? 96 : kLdsRows;
   // rows per step: 32, or 16 when 32-row slots would leave a ring shallower than 2
-  static constexpr int TR = kRingRows / (KW * 32) < 2 ? 16 : 32;
-  static constexpr int PFK = TR == 16 ? 4 : SAS_PFK;        // K operand reads ahead
-  static constexpr int PFV = TR == 16 ? 8 : SAS_PFV;        // V^T operand reads ahead
+  static constexpr int TR = F8R ? 32 : kRingRows / (KW * 32) < 2 ? 16 : 32;
+  static constexpr int PFK = F8R ? SAS_F8_PFK : TR == 16 ? 4 : SAS_PFK;   // K operand reads ahead
+  static constexpr int PFV = F8R ? SAS_F8_PFV : TR == 16 ? 8 : SAS_PFV;   // V^T operand reads ahead
   // two QK^T accumulation chains (one suffices for the half k-range of a
   // channel-split wave, which shares its SIMD with a second wave)
   static constexpr bool CH2 = !QS;
@@ -84,7 +99,7 @@ struct Cfg {
   // computes S for both their head tiles over one 16-row half of the step
   // (two MFMAs per K fragment read, half the K reads of a wave per head),
   // and the S pieces meet in LDS in the layout P.V reads.
-  static constexpr bool Q2 = QS && TR == 32 && HW % 2 == 0;
+  static constexpr bool Q2 = QS && TR == 32 && HW % 2 == 0 && !F8R;
   static constexpr int NQ = Q2 ? 2 : 1;                     // head tiles in a wave's QK^T
   // 8 waves: the workgroup's query rows reach LDS by DMA (waves 4-7, which
   // do no slot resolution), one row per head from row kQRow0 on, in the
@@ -93,8 +108,16 @@ struct Cfg {
   static constexpr bool QL = QS;
   static constexpr int kQRow0 = kLdsRows - 16 * HW;
   static constexpr int MT = TR / 16;                        // 16-key tiles per step
-  static constexpr int NST = kRingRows / (KW * TR) > 4 ? 4 : kRingRows / (KW * TR);   // ring depth per key-group
-  static constexpr int SLOT = TR * kChunksMax;              // slot stride (chunks)
+  static constexpr int NST = F8R ? 3 : kRingRows / (KW * TR) > 4 ? 4 : kRingRows / (KW * TR);   // ring depth per key-group
+  // fp8-resident slot (chunks): latent [32 rows][32], rope [32][8], scales
+  // [32][1], padded to whole DMA instructions (21 x 64)
+  static constexpr int kF8Lat = 0, kF8Rope = 1024, kF8Scl = 1280, kF8Used = 1312, kF8Slot = 1344;
+  static constexpr int SLOT = F8R ? kF8Slot : TR * kChunksMax;   // slot stride (chunks)
+  // S exchange buffers and the query rows (chunk offsets in lds_ring): above
+  // the ring; F8R: the exchange after the last slot, the query rows from the
+  // last key-group's third slot (not in the first fill) on
+  static constexpr int kXsChunk = F8R ? KW * NST * SLOT : kRingRows * kChunksMax;
+  static constexpr int kQChunk = F8R ? (KW - 1) * NST * SLOT + (NST - 1) * SLOT : kQRow0 * kChunksMax;
   static constexpr int CH = D / 8;                          // 16-byte chunks per bf16 row
   static constexpr int KS = D / 32;                         // QK^T k-steps
   // k-steps of one wave. fp8 rows: S is summed per 128-channel scale group
@@ -104,21 +127,26 @@ struct Cfg {
   static constexpr int KSQ = QS ? (KVF ? 10 : KS / 2) : KS;
   static constexpr int NLG = QS ? 2 : 4;                    // fp8: scale groups per wave
   static constexpr int GT = WK * 64;                        // threads per key-group
-  static constexpr int NI = TR * CH / 64;                   // DMA instructions per step
+  static constexpr int NI = F8R ? kF8Slot / 64 : TR * CH / 64;   // DMA instructions per step
   static constexpr int OPS = (NI + WK - 1) / WK;            // most DMA ops per wave per step
   static constexpr int ROWB = KVF ? kRow656 : D * 2;
   // fp8 register staging: 40 work chunks per row (32 latent x 16 values, 8 rope)
   static constexpr int FCPR = 40;
   static constexpr int FOPS = (TR * FCPR + GT - 1) / GT;
-  static_assert(TR * CH % 64 == 0, "whole DMA instructions");
+  static_assert(F8R || TR * CH % 64 == 0, "whole DMA instructions");
   static_assert(!KVF || (KS == 18 && CH == kChunksMax), "fp8 rows: 512 latent + 64 rope channels");
+  static_assert(!F8R || (QS && !Q2 && KW == 2 && NW == 8 && kF8Slot % 64 == 0 && TR == 32),
+                "fp8-resident slots: the 8-wave, two-key-group plan");
+  static_assert(!F8R || (kXsChunk + NW * 64 * MT <= kLdsRows * kChunksMax &&
+                         kQChunk + 16 * HW * CH <= kLdsRows * kChunksMax),
+                "fp8-resident ring, S exchange and query rows fit");
   static_assert(NST >= 2 && NST <= 4, "ring depth");
   static_assert((NST - 1) * OPS < 64, "vmcnt range");
-  static_assert(KW * NST * SLOT <= kRingRows * kChunksMax, "ring fits");
-  static_assert(!QS || (KS % 2 == 0 && NW * 64 * MT * 4 * 4 <= (kLdsRows - kRingRows) * kChunksMax * 16),
+  static_assert(F8R || KW * NST * SLOT <= kRingRows * kChunksMax, "ring fits");
+  static_assert(F8R || !QS || (KS % 2 == 0 && NW * 64 * MT * 4 * 4 <= (kLdsRows - kRingRows) * kChunksMax * 16),
                 "S exchange fits above the ring");
-  // the last key-group's first fill (slots 0 .. NST - 2) ends at or before kQRow0
-  static_assert(!QL || (NW == 8 && (KW - 1) * NST * TR + (NST - 1) * TR <= kQRow0),
+  // the last key-group's first fill (slots 0 .. NST - 2) ends at or before the query rows
+  static_assert(!QL || (NW == 8 && (KW - 1) * NST * SLOT + (NST - 1) * SLOT <= kQChunk),
                 "query rows clear of the first fill");
 };
 
@@ -134,8 +162,8 @@ struct Fwd {
   uint4 qf[C::NQ][C::KSQ];   // Q^T operand of the wave's QK^T head tiles
   float m_run, l_run;
   f32x4 acc[C::NTL];
-  uint4 fbuf[KVF ? C::FOPS : 1];
-  float fsc[KVF ? C::FOPS : 1];
+  uint4 fbuf[KVF == 1 ? C::FOPS : 1];
+  float fsc[KVF == 1 ? C::FOPS : 1];
 
   // wave = kw * WK + jw, jw = cs * HW + hw; wave jw of a key-group issues the
   // DMA instructions i = jw, jw + WK, ... of every step (nops of them)
@@ -164,6 +192,30 @@ struct Fwd {
     const int P = (o * C::WK + jw) * 64 + lane, r = P / C::CH;
     return (uint32_t)(((P - r * C::CH) ^ swz<C::CH>(r)) * 16);
   }
+  // -- fp8-resident slots (F8R) ----------------------------------------------
+  // Slot chunk position P of a step (0 .. kF8Slot): latent chunk (P & 31) ^
+  // swz8l(row) of row P >> 5 below kF8Rope; rope chunk (q & 7) ^ swz8r(row) of
+  // row q >> 3, q = P - kF8Rope, below kF8Scl; the scale chunk of row P -
+  // kF8Scl below kF8Used; past it row 0, chunk 0 (padding, never read).
+  // swz8l is a bijection of the 32 rows onto the 32 latent chunk columns
+  // (even for rows 0-15, odd for 16-31), so a 16-row K read (two chunks per
+  // row) and the 32-row transposed V read (one chunk per row) each touch 32
+  // distinct columns.
+  static __device__ __forceinline__ int swz8l(int r) { return ((r << 1) | (r >> 4)) & 31; }
+  static __device__ __forceinline__ int swz8r(int r) { return (r >> 1) & 7; }
+  __device__ __forceinline__ int drow8(int o) const {
+    const int P = (o * C::WK + jw) * 64 + lane;
+    return P < C::kF8Rope ? P >> 5 : P < C::kF8Scl ? (P - C::kF8Rope) >> 3 : P < C::kF8Used ? P - C::kF8Scl : 0;
+  }
+  __device__ __forceinline__ uint32_t dcol8(int o) const {
+    const int P = (o * C::WK + jw) * 64 + lane;
+    if (P < C::kF8Rope) return (uint32_t)(((P & 31) ^ swz8l(P >> 5)) * 16);
+    if (P < C::kF8Scl) {
+      const int q = P - C::kF8Rope;
+      return 528u + (uint32_t)(((q & 7) ^ swz8r(q >> 3)) * 16);
+    }
+    return P < C::kF8Used ? 512u : 0u;
+  }
   struct Dma {
     uint64_t ra[C::OPS];   // row address of each of the wave's instructions
     uint32_t lds;          // LDS byte address of the slot
@@ -178,7 +230,7 @@ struct Fwd {
       const uint32_t rb = __builtin_amdgcn_readfirstlane(lds_addr_of(lds_rows + rp));
 #pragma unroll
       for (int o = 0; o < C::OPS; ++o)
-        d.ra[o] = *reinterpret_cast<const LDS_AS uint64_t*>((size_t)(rb + 8u * (uint32_t)drow(o)));
+        d.ra[o] = *reinterpret_cast<const LDS_AS uint64_t*>((size_t)(rb + 8u * (uint32_t)(C::F8R ? drow8(o) : drow(o))));
     } else {
       const int last = rp + min(C::TR, nrows - step * C::TR) - 1;   // nk >= 1 for every issued step
 #pragma unroll
@@ -188,7 +240,7 @@ struct Fwd {
   }
   __device__ __forceinline__ void fire(const Dma& d, int o) const {
     if (C::NI % C::WK && o * C::WK + jw >= C::NI) return;   // wave-uniform
-    dma16(reinterpret_cast<const void*>(d.ra[o] + dcol(o)),
+    dma16(reinterpret_cast<const void*>(d.ra[o] + (C::F8R ? dcol8(o) : dcol(o))),
           __builtin_amdgcn_readfirstlane(d.lds + (o * C::WK + jw) * 64 * 16));
   }
   __device__ __forceinline__ void issue(int j, int step) {
@@ -206,7 +258,7 @@ struct Fwd {
     constexpr int NIQ = 16 * HW * C::CH / 64;   // DMA instructions
     static_assert(NIQ * 64 == 16 * HW * C::CH, "whole instructions");
     const uint8_t* qb = p.q + ((size_t)k.t * p.H + k.hg * 16 * HW) * D * 2;
-    const uint32_t lb = lds_addr_of(&lds_ring[C::kQRow0 * kChunksMax]);
+    const uint32_t lb = lds_addr_of(&lds_ring[C::kQChunk]);
     for (int i = wave - 4; i < NIQ; i += 4) {   // wave-uniform
       const int P = i * 64 + lane, r = P / C::CH, pc = P - r * C::CH;
       dma16(qb + (size_t)r * D * 2 + (pc ^ swz<C::CH>(r)) * 16, __builtin_amdgcn_readfirstlane(lb + i * 64 * 16));
@@ -218,7 +270,7 @@ struct Fwd {
     for (int n = 0; n < C::NQ; ++n) {
       const int h = (C::Q2 ? (hw & ~1) + n : hw) * 16 + c16;   // head in the group
       const int hsw = swz<C::CH>(h);
-      const uint4* qr = &lds_ring[C::kQRow0 * kChunksMax + h * C::CH];
+      const uint4* qr = &lds_ring[C::kQChunk + h * C::CH];
 #pragma unroll
       for (int ks = 0; ks < C::KSQ; ++ks) {
         const int L = 4 * kglob(ks) + g;
@@ -599,6 +651,144 @@ struct Fwd {
     }
   }
 
+
+  // -- fp8-resident QK^T (F8R) -------------------------------------------------
+  // As qk for this wave's 16 heads over both 16-row tiles of the step and
+  // its channel half's ten k-steps (two scale groups, then the rope k-steps:
+  // zero Q in half 1). A latent k-step's K fragment is 8 fp8 bytes of the
+  // lane's row (ds_read_b64), read kPfK k-steps ahead and converted to bf16
+  // (exact, unscaled) just before its MFMA; each group's four-k-step chain
+  // is folded into S with the rows' fp32 scale of that group, as in qk.
+  // Rope fragments are bf16 already.
+  template <typename DmaFn>
+  __device__ __forceinline__ void qk8(int sl, f32x4 (&sacc)[C::MT], DmaFn&& dma) {
+    static_assert(!C::Q2 && C::MT == 2 && C::KSQ == 10 && C::NLG == 2, "fp8-resident QK^T layout");
+    constexpr int MT = C::MT;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) sacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint32_t lat[MT], rop[MT];
+    int sw[MT], swr[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = mt * 16 + c16;
+      lat[mt] = lds_addr_of(&lds_ring[sl + C::kF8Lat + r * 32]) + 8u * (uint32_t)(g & 1);
+      rop[mt] = lds_addr_of(&lds_ring[sl + C::kF8Rope + r * 8]);
+      sw[mt] = swz8l(r);
+      swr[mt] = swz8r(r);
+    }
+    // scale of group 2 cs + lg of key row k: float 4 k + 2 cs + lg of the scale chunks
+    const float* sc = reinterpret_cast<const float*>(&lds_ring[sl + C::kF8Scl]) + 2 * cs;
+    auto kraw = [&](int ks, int mt) -> uint4 {
+      if (ks < 8) {
+        const int c = 2 * (cs * 8 + ks) + (g >> 1);   // latent chunk of channels 32 k + 8 g ..
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v = *reinterpret_cast<const LDS_AS u32x2*>((size_t)(lat[mt] + (uint32_t)((c ^ sw[mt]) * 16)));
+        return make_uint4(v.x, v.y, 0u, 0u);
+      }
+      const int c = 4 * (ks - 8) + g;                 // rope chunk of channels 512 + 32 k' + 8 g ..
+      typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 v = *reinterpret_cast<const LDS_AS u32x4*>((size_t)(rop[mt] + (uint32_t)((c ^ swr[mt]) * 16)));
+      return make_uint4(v.x, v.y, v.z, v.w);
+    };
+    constexpr int kPfK = C::PFK;
+    uint4 af[kPfK][MT];
+#pragma unroll
+    for (int i = 0; i < kPfK; ++i)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) af[i][mt] = kraw(i, mt);
+    f32x4 gacc[MT];
+#pragma unroll
+    for (int ks = 0; ks < C::KSQ; ++ks) {
+      uint4 raw[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) raw[mt] = af[ks % kPfK][mt];
+      if (ks + kPfK < C::KSQ) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) af[ks % kPfK][mt] = kraw(ks + kPfK, mt);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        uint4 a = raw[mt];
+        if (ks < 8) {
+          uint32_t o0, o1, o2, o3;
+          e4m3x4_to_bf16(raw[mt].x, o0, o1);
+          e4m3x4_to_bf16(raw[mt].y, o2, o3);
+          a = make_uint4(o0, o1, o2, o3);
+          gacc[mt] = mfma32k<QT>(a, qf[0][ks], ks % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : gacc[mt]);
+        } else {
+          sacc[mt] = mfma32k<QT>(a, qf[0][ks], sacc[mt]);
+        }
+      }
+      if (ks == 3 || ks == 7) {
+        const int lg = ks / 4;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int k0 = mt * 16 + 4 * g;
+          const f32x4 f = {sc[4 * k0 + lg], sc[4 * (k0 + 1) + lg], sc[4 * (k0 + 2) + lg], sc[4 * (k0 + 3) + lg]};
+          sacc[mt] += f * gacc[mt];
+        }
+      }
+      if ((ks & 1) && ks / 2 < C::OPS) dma(ks / 2);
+    }
+#pragma unroll
+    for (int o = C::KSQ / 2; o < C::OPS; ++o) dma(o);
+  }
+
+  // -- fp8-resident P.V (F8R) --------------------------------------------------
+  // O^T += V^T . P^T over the step's 32 keys, one 16x16x32 MFMA per 16-channel
+  // tile of the wave's channel half. The lane's P holds keys kappa(g, s) =
+  // 4 g + s (s < 4) and 16 + 4 g + s - 4 (s >= 4) of head c16; the V^T
+  // fragment must hold the same keys of channel c16 of the tile. The 8-bit
+  // transposed read gives lane j of each 16-lane group byte j % 8 of the
+  // addresses of lanes 2 s + (j >= 8), s = 0 .. 7: so lane (g, c16) points
+  // at key row kappa(g, c16 >> 1), bytes 8 (c16 & 1) .. of the tile's chunk,
+  // and receives channel c16 of its group's eight keys in kappa order. The
+  // fp8 values are converted at use; P is scaled per group as in pv.
+  __device__ __forceinline__ void pv8(int sl, const uint32_t (&pk)[2 * C::MT]) {
+    static_assert(C::MT == 2 && C::NLG == 2 && C::NTL == 16, "fp8-resident P.V layout");
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    const int s = c16 >> 1;
+    const int kr = s < 4 ? 4 * g + s : 12 + 4 * g + s;
+    const uint32_t vrow = lds_addr_of(&lds_ring[sl + C::kF8Lat + kr * 32]) + 8u * (uint32_t)(c16 & 1);
+    const int sw = swz8l(kr);
+    // P x scale of group 2 cs + lg for the lane's keys (4 g + i, 16 + 4 g + i)
+    uint32_t pks[2][4];
+    {
+      // scale of group 2 cs + lg of key row k: float 4 k + 2 cs + lg of the scale chunks
+      const float* sc = reinterpret_cast<const float*>(&lds_ring[sl + C::kF8Scl]) + 2 * cs;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int lg = 0; lg < 2; ++lg)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int k0 = mt * 16 + 4 * g + 2 * h;
+            const uint32_t w = pk[mt * 2 + h];
+            pks[lg][mt * 2 + h] = pack2<QT>(__uint_as_float(w << 16) * sc[4 * k0 + lg],
+                                            __uint_as_float(w & 0xffff0000u) * sc[4 * (k0 + 1) + lg]);
+          }
+    }
+    auto vraw = [&](int mt) -> v2i {
+      const int c = cs * 16 + mt;   // latent chunk of channels 16 c .. 16 c + 15
+      return __builtin_amdgcn_ds_read_tr8_b64_v2i32((LDS_AS v2i*)(size_t)(vrow + (uint32_t)((c ^ sw) * 16)));
+    };
+    constexpr int kPfV = C::PFV;
+    v2i vf[kPfV];
+#pragma unroll
+    for (int i = 0; i < kPfV; ++i) vf[i] = vraw(i);
+#pragma unroll
+    for (int mt = 0; mt < C::NTL; ++mt) {
+      const v2i raw = vf[mt % kPfV];
+      if (mt + kPfV < C::NTL) vf[mt % kPfV] = vraw(mt + kPfV);
+      uint32_t o0, o1, o2, o3;
+      e4m3x4_to_bf16((uint32_t)raw.x, o0, o1);
+      e4m3x4_to_bf16((uint32_t)raw.y, o2, o3);
+      const int lg = mt / 8;
+      acc[mt] = mfma32k<QT>(make_uint4(o0, o1, o2, o3), make_uint4(pks[lg][0], pks[lg][1], pks[lg][2], pks[lg][3]),
+                            acc[mt]);
+    }
+  }
+
   // One step. With QS the two halves of S meet in LDS (one barrier, taken by
   // every wave of the workgroup whether or not its key-group has the step).
   template <typename DmaFn>
@@ -606,9 +796,13 @@ struct Fwd {
     f32x4 sacc[C::MT], sodd[C::MT];
     uint32_t pk[2 * C::MT];
     const bool live = C::KW == 1 || step < nsteps;   // one key-group: every step is live
-    if (live) qk(sl, sacc, sodd, dma);
+    if constexpr (C::F8R) {
+      if (live) qk8(sl, sacc, dma);
+    } else {
+      if (live) qk(sl, sacc, sodd, dma);
+    }
     if constexpr (C::QS) {
-      f32x4* xs = reinterpret_cast<f32x4*>(lds_ring + C::kRingRows * kChunksMax);
+      f32x4* xs = reinterpret_cast<f32x4*>(lds_ring + C::kXsChunk);
       const int wave = kw * C::WK + jw;
       const int other = wave ^ HW;   // same heads, other channel half
       // Q2 piece (head tile ht, row tile rt, channel half c) of this key-group
@@ -632,7 +826,8 @@ struct Fwd {
         smax_a<false>(sacc, sodd, step, sv);
 #pragma unroll
         for (int e = 0; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
-        pv(sl, pk, [](int) {});
+        if constexpr (C::F8R) pv8(sl, pk);
+        else pv(sl, pk, [](int) {});
       }
       return;
     }
@@ -655,7 +850,7 @@ struct Fwd {
   __device__ __forceinline__ void step_j(int it0) {
     const int it = it0 + J;
     if (it >= nsteps_max) return;   // uniform over the workgroup (HW > 1) / wave
-    if constexpr (!KVF) {
+    if constexpr (KVF != 1) {
       // Steps up to it + NST - 2 have been issued. My DMA for step `it` done
       // (the later ones may still stream), then all waves: every wave has
       // finished step it - 1, so its slot (J + NST - 1) % NST takes step
@@ -824,7 +1019,7 @@ struct Fwd {
   // two (step + exchange).
   static constexpr bool kPipe8 = !KVF && C::Q2 && C::KW == 1 && C::NST == 3 && NW == 8;
   __device__ __forceinline__ f32x4* xs_buf(int b) const {
-    return reinterpret_cast<f32x4*>(lds_ring + C::kRingRows * kChunksMax) + b * (NW * C::MT * 64);
+    return reinterpret_cast<f32x4*>(lds_ring + C::kXsChunk) + b * (NW * C::MT * 64);
   }
   // Q2 piece (head tile ht, row tile rt, channel half c)
   __device__ __forceinline__ int piece(int ht, int rt, int c) const { return ((ht * 2 + rt) * 2 + c) * 64 + lane; }
@@ -913,7 +1108,7 @@ struct Fwd {
       run_pipe8();
       return;
     }
-    if constexpr (!KVF) {
+    if constexpr (KVF != 1) {
 #pragma unroll
       for (int j = 0; j < C::NST - 1; ++j)
         if (j < nsteps) issue(j, j);
@@ -1236,7 +1431,7 @@ sas_fwd_kernel(const FwdParams p) {
   const int nvalid = __builtin_amdgcn_readfirstlane(k.nvalid);
   // QL kernels: pad lds_rows with copies of the last row (read after the
   // query barrier below; with no rows no step is issued)
-  if constexpr (C::QL && !KVF) {
+  if constexpr (C::QL && KVF != 1) {
     static_assert(2 * C::TR <= kRowPad, "a step past the last reaches at most 2 TR entries beyond it");
     if (tid < kRowPad) lds_rows[nvalid + tid] = lds_rows[nvalid > 0 ? nvalid - 1 : 0];
   }
@@ -1641,7 +1836,8 @@ int dispatch_hw(int hw, int nw, bool exact, const FwdParams& fp, int nb, hipStre
   }
   if (hw == 2 && nw == 4) return launch_fwd<2, 4, D, QT, KVF>(fp, nb, st);
   if (hw == 4 && nw == 4) return launch_fwd<4, 4, D, QT, KVF>(fp, nb, st);
-  if (hw == 2 && nw == 8) return launch_fwd<2, 8, D, QT, KVF>(fp, nb, st);
+  // fp8 rows in the 32-head 8-wave plan: kept as fp8 in LDS (KVF 2)
+  if (hw == 2 && nw == 8) return launch_fwd<2, 8, D, QT, KVF ? SAS_FP8_RESIDENT : 0>(fp, nb, st);
   if (hw == 4 && nw == 8) return launch_fwd<4, 8, D, QT, KVF>(fp, nb, st);
   return sas::set_error(SAS_EINVAL, "unsupported head grouping");
 }

@@ -58,9 +58,20 @@ def _instrument(src: str) -> str:
             "  float m_run, l_run;\n  f32x4 acc[C::NTL];\n"
             "  unsigned long long ph[8] = {0, 0, 0, 0, 0, 0, 0, 0};\n  unsigned long long c2 = 0, pro = 0;")
     # compute(): QK, exchange barrier, softmax, P.V of the channel-split step
-    s = rep(s, "    if (live) qk(sl, sacc, sodd, dma);\n    if constexpr (C::QS) {",
-            "    const unsigned long long ta = CT();\n    if (live) qk(sl, sacc, sodd, dma);\n"
-            "    const unsigned long long tb = CT();\n    ph[1] += tb - ta;\n    if constexpr (C::QS) {")
+    s = rep(s, """    if constexpr (C::F8R) {
+      if (live) qk8(sl, sacc, dma);
+    } else {
+      if (live) qk(sl, sacc, sodd, dma);
+    }
+    if constexpr (C::QS) {""", """    const unsigned long long ta = CT();
+    if constexpr (C::F8R) {
+      if (live) qk8(sl, sacc, dma);
+    } else {
+      if (live) qk(sl, sacc, sodd, dma);
+    }
+    const unsigned long long tb = CT();
+    ph[1] += tb - ta;
+    if constexpr (C::QS) {""")
     s = rep(s, """      lds_barrier();
       if (live) {
 #pragma unroll
@@ -74,12 +85,14 @@ def _instrument(src: str) -> str:
         for (int mt = 0; mt < C::MT; ++mt) {
           if constexpr (C::Q2) sacc[mt] = xs[piece(hw, mt, 0)] + xs[piece(hw, mt, 1)];""")
     s = rep(s, """        for (int e = 0; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
-        pv(sl, pk, [](int) {});
+        if constexpr (C::F8R) pv8(sl, pk);
+        else pv(sl, pk, [](int) {});
       }
       return;""", """        for (int e = 0; e < kSmaxB; ++e) smax_b(e, sv, lsum, pk);
         const unsigned long long td = CT();
         ph[3] += td - tc;
-        pv(sl, pk, [](int) {});
+        if constexpr (C::F8R) pv8(sl, pk);
+        else pv(sl, pk, [](int) {});
         ph[4] += CT() - td;
       }
       return;""")
