@@ -166,10 +166,12 @@ __global__ void __launch_bounds__(256 * NG) sas_bwd_kernel(const BwdParams bp) {
                                                      ((size_t)t * p.H + k.hg * NHD) * D);
     const uint4* ds = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(bp.dout) +
                                                      ((size_t)t * p.H + k.hg * NHD) * kDV);
-    for (int i = tid; i < NHD * D / 8; i += NT)
-      *reinterpret_cast<uint4*>(lds_q + (i / (D / 8)) * QS + (i % (D / 8)) * 16) = qs[i];
-    for (int i = tid; i < NHD * kDV / 8; i += NT)
-      *reinterpret_cast<uint4*>(lds_do + (i / (kDV / 8)) * OS + (i % (kDV / 8)) * 16) = ds[i];
+    stage_chunks<NHD * D / 8, NT>(qs, tid, [&](int i, const uint4& v) {
+      *reinterpret_cast<uint4*>(lds_q + (i / (D / 8)) * QS + (i % (D / 8)) * 16) = v;
+    });
+    stage_chunks<NHD * kDV / 8, NT>(ds, tid, [&](int i, const uint4& v) {
+      *reinterpret_cast<uint4*>(lds_do + (i / (kDV / 8)) * OS + (i % (kDV / 8)) * 16) = v;
+    });
   }
   const float scale = p.scale_log2 / kLog2e;
   const uint64_t ori_lo = reinterpret_cast<uint64_t>(p.ori_kv);
@@ -399,8 +401,9 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
   {
     const uint4* qg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.q) +
                                                      ((size_t)t * p.H + h0) * D);
-    for (int i = tid; i < NHD * CH; i += NT)
-      *reinterpret_cast<uint4*>(lds_qo + (i / CH) * QSTR + (i % CH) * 16) = qg[i];
+    stage_chunks<NHD * CH, NT>(qg, tid, [&](int i, const uint4& v) {
+      *reinterpret_cast<uint4*>(lds_qo + (i / CH) * QSTR + (i % CH) * 16) = v;
+    });
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < KSH; ++ks)
@@ -415,8 +418,9 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
     __syncthreads();   // every wave has its q before dO overwrites it
     const uint4* ds = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(bp.dout) +
                                                      ((size_t)t * p.H + h0) * kDV);
-    for (int i = tid; i < NHD * kDV / 8; i += NT)
-      *reinterpret_cast<uint4*>(lds_qo + (i / (kDV / 8)) * OS + (i % (kDV / 8)) * 16) = ds[i];
+    stage_chunks<NHD * kDV / 8, NT>(ds, tid, [&](int i, const uint4& v) {
+      *reinterpret_cast<uint4*>(lds_qo + (i / (kDV / 8)) * OS + (i % (kDV / 8)) * 16) = v;
+    });
   }
   const float scale = p.scale_log2 / kLog2e;
   const uint64_t ori_lo = reinterpret_cast<uint64_t>(p.ori_kv);

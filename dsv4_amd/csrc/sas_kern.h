@@ -229,6 +229,23 @@ __device__ __forceinline__ void wait_vm() {
 __device__ __forceinline__ void wait_lgkm0() {
   __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
 }
+// N 16-byte chunks from global memory into LDS by NT threads: every load is
+// issued (at a clamped, in-range index) before the first LDS write, so the
+// copy costs one round trip. (A strided copy loop compiled to load, wait,
+// write per pass: nine round trips for a 64-head query tile.)
+template <int N, int NT, typename Put>
+__device__ __forceinline__ void stage_chunks(const uint4* src, int tid, Put&& put) {
+  constexpr int NIT = (N + NT - 1) / NT;
+  uint4 v[NIT];
+#pragma unroll
+  for (int j = 0; j < NIT; ++j) v[j] = src[min(tid + j * NT, N - 1)];
+#pragma unroll
+  for (int j = 0; j < NIT; ++j) {
+    const int i = tid + j * NT;
+    if (N % NT == 0 || i < N) put(i, v[j]);
+  }
+}
+
 // LDS reads done, then a workgroup barrier (no memory fence: in-flight LDS
 // DMA of other slots keeps streaming across it).
 __device__ __forceinline__ void lds_barrier() {
