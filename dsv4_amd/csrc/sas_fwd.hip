@@ -99,7 +99,7 @@ struct Cfg {
   // computes S for both their head tiles over one 16-row half of the step
   // (two MFMAs per K fragment read, half the K reads of a wave per head),
   // and the S pieces meet in LDS in the layout P.V reads.
-  static constexpr bool Q2 = QS && TR == 32 && HW % 2 == 0 && !F8R;
+  static constexpr bool Q2 = QS && TR == 32 && HW % 2 == 0;
   static constexpr int NQ = Q2 ? 2 : 1;                     // head tiles in a wave's QK^T
   // 8 waves: the workgroup's query rows reach LDS by DMA (waves 4-7, which
   // do no slot resolution), one row per head from row kQRow0 on, in the
@@ -124,7 +124,7 @@ struct Cfg {
   // (4 k-steps) and each group's sum scaled in fp32, so a channel split
   // follows the groups: half 0 takes groups 0-1 and the two rope k-steps,
   // half 1 groups 2-3 and two k-steps of zero Q (10 each).
-  static constexpr int KSQ = QS ? (KVF ? 10 : KS / 2) : KS;
+  static constexpr int KSQ = QS ? (F8R ? 9 : KVF ? 10 : KS / 2) : KS;
   static constexpr int NLG = QS ? 2 : 4;                    // fp8: scale groups per wave
   static constexpr int GT = WK * 64;                        // threads per key-group
   static constexpr int NI = F8R ? kF8Slot / 64 : TR * CH / 64;   // DMA instructions per step
@@ -135,8 +135,8 @@ struct Cfg {
   static constexpr int FOPS = (TR * FCPR + GT - 1) / GT;
   static_assert(F8R || TR * CH % 64 == 0, "whole DMA instructions");
   static_assert(!KVF || (KS == 18 && CH == kChunksMax), "fp8 rows: 512 latent + 64 rope channels");
-  static_assert(!F8R || (QS && !Q2 && KW == 2 && NW == 8 && kF8Slot % 64 == 0 && TR == 32),
-                "fp8-resident slots: the 8-wave, two-key-group plan");
+  static_assert(!F8R || (QS && Q2 && KW == 2 && NW == 8 && kF8Slot % 64 == 0 && TR == 32),
+                "fp8-resident slots: the 8-wave, two-key-group, paired-QK^T plan");
   static_assert(!F8R || (kXsChunk + NW * 64 * MT <= kLdsRows * kChunksMax &&
                          kQChunk + 16 * HW * CH <= kLdsRows * kChunksMax),
                 "fp8-resident ring, S exchange and query rows fit");
@@ -177,7 +177,11 @@ struct Fwd {
   // computes (fp8 channel halves: local k-steps 8 and 9 are the rope k-steps
   // 16 and 17, with zero Q in half 1)
   __device__ __forceinline__ int kbase() const { return C::QS ? (KVF ? cs * 8 : cs * C::KSQ) : 0; }
-  __device__ __forceinline__ int kglob(int ks) const { return (KVF && C::QS && ks >= 8) ? ks + 8 : kbase() + ks; }
+  // (fp8-resident: channel half cs takes latent groups 2 cs, 2 cs + 1 and
+  // rope k-step 16 + cs, nine k-steps each)
+  __device__ __forceinline__ int kglob(int ks) const {
+    return (KVF && C::QS && ks >= 8) ? (C::F8R ? 16 + cs : ks + 8) : kbase() + ks;
+  }
 
   // -- bf16 / fp16 rows: DMA one step into slot j ------------------------------
   // Lane `lane` of the wave's o-th instruction of a step moves row drow(o) of
@@ -275,7 +279,7 @@ struct Fwd {
       for (int ks = 0; ks < C::KSQ; ++ks) {
         const int L = 4 * kglob(ks) + g;
         qf[n][ks] = qr[(L & -SG) | ((L & (SG - 1)) ^ hsw)];
-        if (KVF && C::QS && ks >= 8 && cs == 1) qf[n][ks] = make_uint4(0, 0, 0, 0);
+        if (KVF == 1 && C::QS && ks >= 8 && cs == 1) qf[n][ks] = make_uint4(0, 0, 0, 0);
       }
     }
   }
@@ -653,80 +657,64 @@ struct Fwd {
 
 
   // -- fp8-resident QK^T (F8R) -------------------------------------------------
-  // As qk for this wave's 16 heads over both 16-row tiles of the step and
-  // its channel half's ten k-steps (two scale groups, then the rope k-steps:
-  // zero Q in half 1). A latent k-step's K fragment is 8 fp8 bytes of the
-  // lane's row (ds_read_b64), read kPfK k-steps ahead and converted to bf16
-  // (exact, unscaled) just before its MFMA; each group's four-k-step chain
-  // is folded into S with the rows' fp32 scale of that group, as in qk.
-  // Rope fragments are bf16 already.
+  // Paired head tiles, as qk with Q2: this wave's 16-row half (hw & 1) of the
+  // step against both head tiles of its pair, over its channel half's nine
+  // k-steps (scale groups 2 cs and 2 cs + 1, then rope k-step 16 + cs). A
+  // latent k-step's K fragment is 8 fp8 bytes of the lane's row
+  // (ds_read_b64), read kPfK k-steps ahead and converted to bf16 (exact,
+  // unscaled) just before its two MFMAs; each group's four-k-step chain is
+  // folded into S with the rows' fp32 scale of that group, as in qk. The
+  // rope fragment is bf16 already.
   template <typename DmaFn>
   __device__ __forceinline__ void qk8(int sl, f32x4 (&sacc)[C::MT], DmaFn&& dma) {
-    static_assert(!C::Q2 && C::MT == 2 && C::KSQ == 10 && C::NLG == 2, "fp8-resident QK^T layout");
+    static_assert(C::Q2 && C::MT == 2 && C::KSQ == 9 && C::NLG == 2, "fp8-resident QK^T layout");
     constexpr int MT = C::MT;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) sacc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    uint32_t lat[MT], rop[MT];
-    int sw[MT], swr[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int r = mt * 16 + c16;
-      lat[mt] = lds_addr_of(&lds_ring[sl + C::kF8Lat + r * 32]) + 8u * (uint32_t)(g & 1);
-      rop[mt] = lds_addr_of(&lds_ring[sl + C::kF8Rope + r * 8]);
-      sw[mt] = swz8l(r);
-      swr[mt] = swz8r(r);
-    }
+    const int r = (hw & 1) * 16 + c16;
+    const uint32_t lat = lds_addr_of(&lds_ring[sl + C::kF8Lat + r * 32]) + 8u * (uint32_t)(g & 1);
+    const uint32_t rop = lds_addr_of(&lds_ring[sl + C::kF8Rope + r * 8]);
+    const int sw = swz8l(r), swr = swz8r(r);
     // scale of group 2 cs + lg of key row k: float 4 k + 2 cs + lg of the scale chunks
     const float* sc = reinterpret_cast<const float*>(&lds_ring[sl + C::kF8Scl]) + 2 * cs;
-    auto kraw = [&](int ks, int mt) -> uint4 {
+    auto kraw = [&](int ks) -> uint4 {
+      typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+      typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
       if (ks < 8) {
         const int c = 2 * (cs * 8 + ks) + (g >> 1);   // latent chunk of channels 32 k + 8 g ..
-        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 v = *reinterpret_cast<const LDS_AS u32x2*>((size_t)(lat[mt] + (uint32_t)((c ^ sw[mt]) * 16)));
+        const u32x2 v = *reinterpret_cast<const LDS_AS u32x2*>((size_t)(lat + (uint32_t)((c ^ sw) * 16)));
         return make_uint4(v.x, v.y, 0u, 0u);
       }
-      const int c = 4 * (ks - 8) + g;                 // rope chunk of channels 512 + 32 k' + 8 g ..
-      typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-      const u32x4 v = *reinterpret_cast<const LDS_AS u32x4*>((size_t)(rop[mt] + (uint32_t)((c ^ swr[mt]) * 16)));
+      const int c = 4 * cs + g;                       // rope chunk of channels 512 + 32 cs + 8 g ..
+      const u32x4 v = *reinterpret_cast<const LDS_AS u32x4*>((size_t)(rop + (uint32_t)((c ^ swr) * 16)));
       return make_uint4(v.x, v.y, v.z, v.w);
     };
     constexpr int kPfK = C::PFK;
-    uint4 af[kPfK][MT];
+    uint4 af[kPfK];
 #pragma unroll
-    for (int i = 0; i < kPfK; ++i)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) af[i][mt] = kraw(i, mt);
+    for (int i = 0; i < kPfK; ++i) af[i] = kraw(i);
     f32x4 gacc[MT];
 #pragma unroll
     for (int ks = 0; ks < C::KSQ; ++ks) {
-      uint4 raw[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) raw[mt] = af[ks % kPfK][mt];
-      if (ks + kPfK < C::KSQ) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) af[ks % kPfK][mt] = kraw(ks + kPfK, mt);
+      const uint4 raw = af[ks % kPfK];
+      if (ks + kPfK < C::KSQ) af[ks % kPfK] = kraw(ks + kPfK);
+      uint4 a = raw;
+      if (ks < 8) {
+        uint32_t o0, o1, o2, o3;
+        e4m3x4_to_bf16(raw.x, o0, o1);
+        e4m3x4_to_bf16(raw.y, o2, o3);
+        a = make_uint4(o0, o1, o2, o3);
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        uint4 a = raw[mt];
-        if (ks < 8) {
-          uint32_t o0, o1, o2, o3;
-          e4m3x4_to_bf16(raw[mt].x, o0, o1);
-          e4m3x4_to_bf16(raw[mt].y, o2, o3);
-          a = make_uint4(o0, o1, o2, o3);
-          gacc[mt] = mfma32k<QT>(a, qf[0][ks], ks % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : gacc[mt]);
-        } else {
-          sacc[mt] = mfma32k<QT>(a, qf[0][ks], sacc[mt]);
-        }
+        if (ks < 8) gacc[mt] = mfma32k<QT>(a, qf[mt][ks], ks % 4 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : gacc[mt]);
+        else sacc[mt] = mfma32k<QT>(a, qf[mt][ks], sacc[mt]);
       }
       if (ks == 3 || ks == 7) {
-        const int lg = ks / 4;
+        const int lg = ks / 4, k0 = (hw & 1) * 16 + 4 * g;
+        const f32x4 f = {sc[4 * k0 + lg], sc[4 * (k0 + 1) + lg], sc[4 * (k0 + 2) + lg], sc[4 * (k0 + 3) + lg]};
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int k0 = mt * 16 + 4 * g;
-          const f32x4 f = {sc[4 * k0 + lg], sc[4 * (k0 + 1) + lg], sc[4 * (k0 + 2) + lg], sc[4 * (k0 + 3) + lg]};
-          sacc[mt] += f * gacc[mt];
-        }
+        for (int mt = 0; mt < MT; ++mt) sacc[mt] += f * gacc[mt];
       }
       if ((ks & 1) && ks / 2 < C::OPS) dma(ks / 2);
     }
