@@ -347,7 +347,13 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
   static_assert(NCT % 2 == 0 && KSH * 2 * 32 == D, "channel halves");
   // q is staged here for the register loads, then dO takes the space
   __shared__ __attribute__((aligned(16))) uint8_t lds_qo[NHD * QSTR];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_k[kBwdRows * KS];
+  // row chunks, double-buffered, filled by LDS-DMA: chunk position P of a
+  // buffer is row P / KCH, 16-byte chunk P % KCH (the last chunk of a padded
+  // row, and positions past the chunk, take a dummy copy)
+  constexpr int KCH = KS / 16;                              // chunks per padded row
+  constexpr int NKDMA = (kBwdRows * KCH + 63) / 64;         // DMA instructions per chunk
+  static_assert(KS % 16 == 0 && KCH == CH + 1, "padded row = chunks + one");
+  __shared__ __attribute__((aligned(16))) uint8_t lds_kb[2][NKDMA * 64 * 16];
   __shared__ float lds_pd[kBwdRows][NHD][2];   // (P, scale dS) per row and head
   __shared__ float lds_hd[NHD][2];             // per head: Delta, lse (log2 units)
   __shared__ f32x4 lds_x[8][2][64];            // S^T / dP^T channel halves per wave
@@ -430,34 +436,48 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
 #pragma unroll
   for (int j = 0; j < DQT; ++j) dqt[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Row chunks double-buffered through registers, as in the 32-head kernel
-  constexpr int NLD = (kBwdRows * CH + NT - 1) / NT;
-  uint4 rbuf[NLD];
-  auto load_rows = [&](int c0n) {
+  // Row chunks by LDS-DMA into two buffers: chunk c + 1 is issued right
+  // after chunk c is in LDS and lands during its compute (rows past the end
+  // repeat the last row: their P and dS are 0). The DMA is not tracked by
+  // the compiler; its completion is waited for explicitly. The only vector-
+  // memory operations a wave issues after its DMA of a chunk are its
+  // row-gradient atomics of the chunk before, natom of them, so waiting
+  // until at most natom operations are in flight (rounded down) covers the
+  // DMA without waiting for the atomics. (With the rows loaded through
+  // registers the compiler waited for everything in flight, the atomics
+  // included: the atomics were issued in branches it could not count.)
+  auto dma_rows = [&](int b, int c0n) {
     const int nrn = min(kBwdRows, k.nvalid - c0n);
-    unroll<NLD>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      const int i = tid + NT * j;
-      if (i < kBwdRows * CH) {
-        const int r = i / CH, c = i - r * CH;
-        rbuf[j] = gld16(lds_rows[c0n + min(r, nrn - 1)] + c * 16);
-      }
-    });
+    const uint32_t rb = __builtin_amdgcn_readfirstlane(lds_addr_of(lds_rows + c0n));
+    const uint32_t kb0 = lds_addr_of(lds_kb[b]);
+    for (int o = wave; o < NKDMA; o += 8) {   // wave-uniform
+      const int P = o * 64 + lane, r = P / KCH, c = P - r * KCH;
+      const bool real = r < kBwdRows && c < CH;
+      const uint64_t a = *reinterpret_cast<const LDS_AS uint64_t*>(
+          (size_t)(rb + 8u * (uint32_t)(real ? min(r, nrn - 1) : 0)));
+      dma16(reinterpret_cast<const void*>(a + (real ? (uint64_t)c * 16 : 0)),
+            __builtin_amdgcn_readfirstlane(kb0 + (uint32_t)o * 64 * 16));
+    }
   };
-  if (k.nvalid > 0) load_rows(0);
+  auto wait_vm_atmost = [](int n) {   // n wave-uniform; rounded down to a multiple of 4
+    if (n >= 16) wait_vm<16>();
+    else if (n >= 12) wait_vm<12>();
+    else if (n >= 8) wait_vm<8>();
+    else if (n >= 4) wait_vm<4>();
+    else wait_vm<0>();
+  };
+  int ntile = 0;   // dkv tiles of this wave: ct = wave + 8 m < NCT
+#pragma unroll
+  for (int m = 0; m < MT; ++m) ntile += wave + 8 * m < NCT;
+  int natom = 0;   // atomic instructions this wave issued since its last DMA
+  if (k.nvalid > 0) dma_rows(0, 0);
 
-  for (int c0 = 0; c0 < k.nvalid; c0 += kBwdRows) {
+  for (int c0 = 0, ci = 0; c0 < k.nvalid; c0 += kBwdRows, ++ci) {
     const int nr = min(kBwdRows, k.nvalid - c0);
-    unroll<NLD>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      const int i = tid + NT * j;
-      if (i < kBwdRows * CH) {
-        const int r = i / CH, c = i - r * CH;
-        *reinterpret_cast<uint4*>(lds_k + r * KS + c * 16) = rbuf[j];
-      }
-    });
-    __syncthreads();   // the chunk (and, the first time, dO) in LDS
-    if (c0 + kBwdRows < k.nvalid) load_rows(c0 + kBwdRows);
+    const uint8_t* lds_k = lds_kb[ci & 1];
+    wait_vm_atmost(natom);   // my DMA of this chunk
+    lds_barrier();           // everyone's (and, the first time, dO) in LDS
+    if (c0 + kBwdRows < k.nvalid) dma_rows((ci + 1) & 1, c0 + kBwdRows);
     // this wave's channel half of S^T = K . Q^T and dP^T = V . dO^T for its
     // head group: A = 8 channels of key c16, B = the same channels of head c16
     {
@@ -474,7 +494,7 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
       }
       lds_x[wave][0][lane] = sacc;
       lds_x[wave][1][lane] = dacc;
-      __syncthreads();
+      lds_barrier();
       sacc += lds_x[wave ^ 1][0][lane];
       dacc += lds_x[wave ^ 1][1][lane];
       // lane (g4, c16): keys 4 g4 .. + 3 of head 16 g + c16; one wave of the
@@ -495,7 +515,7 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     // dq[head][ch] += dS[head][key] . K[key][ch] over this wave's head group
     // and channel half (A = keys 4 g4 .. + 3 of head c16; B = the same keys
     // of channel 16 ct + c16, rows past nr carry dS = 0)
@@ -533,6 +553,11 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
       }
       // a chunk of window rows only, under the window pass: no dkv here
       const bool any_row = __ballot(grow[0] || grow[1] || grow[2] || grow[3]) != 0;
+      // the atomic instructions issued below: one per (tile, i) with some lane's row
+      int nrow_i = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) nrow_i += __ballot(grow[i] != nullptr) != 0;
+      natom = any_row ? ntile * nrow_i : 0;
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         const int ct = wave + 8 * m;
@@ -549,7 +574,7 @@ __global__ void __launch_bounds__(512) sas_bwd64_kernel(const BwdParams bp) {
           if (grow[i]) atomicAdd(grow[i] + ch, acc[i]);
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   // one split: the workgroup owns its heads' dq; several: each adds its share
   float* dqb = bp.dq + ((size_t)t * p.H + h0 + 16 * g + 4 * g4) * D + c16;
