@@ -55,6 +55,9 @@
 #ifndef SAS_PFV
 #define SAS_PFV 4   // V^T operand channel tiles read ahead (32-row steps)
 #endif
+#ifndef SAS_KSPLIT
+#define SAS_KSPLIT 1   // 64-head 8-wave plan: QK^T split across the wave pair by keys (1) or channels (0)
+#endif
 
 
 namespace sas {
@@ -86,6 +89,12 @@ struct Cfg {
   // halves through LDS (no QK^T work is duplicated). The exchange buffer
   // takes the ring rows above kRingRows.
   static constexpr bool QS = CS == 2;
+  // Key-split QK^T (the 64-head, 8-wave, one-key-group plan with
+  // SAS_KSPLIT): the two waves of a pair each compute S over all D channels
+  // for one 16-key half of the step, run the softmax of their own keys and
+  // exchange P (with their reference max) instead of S halves; O stays
+  // split by channels.
+  static constexpr bool KSP = SAS_KSPLIT && !KVF && NW == 8 && HW == 4;
   static constexpr int kRingRows = QS ? 96 : kLdsRows;
   // rows per step: 32, or 16 when 32-row slots would leave a ring shallower than 2
   static constexpr int TR = F8R ? 32 : kRingRows / (KW * 32) < 2 ? 16 : 32;
@@ -93,13 +102,13 @@ struct Cfg {
   static constexpr int PFV = F8R ? SAS_F8_PFV : TR == 16 ? 8 : SAS_PFV;   // V^T operand reads ahead
   // two QK^T accumulation chains (one suffices for the half k-range of a
   // channel-split wave, which shares its SIMD with a second wave)
-  static constexpr bool CH2 = !QS;
+  static constexpr bool CH2 = !QS || KSP;
   // Paired QK^T (channel-split waves, 32-row steps): the head-waves 2h and
   // 2h + 1 of a channel half share their K operand reads. Each of the two
   // computes S for both their head tiles over one 16-row half of the step
   // (two MFMAs per K fragment read, half the K reads of a wave per head),
   // and the S pieces meet in LDS in the layout P.V reads.
-  static constexpr bool Q2 = QS && TR == 32 && HW % 2 == 0;
+  static constexpr bool Q2 = QS && TR == 32 && HW % 2 == 0 && !KSP;
   static constexpr int NQ = Q2 ? 2 : 1;                     // head tiles in a wave's QK^T
   // 8 waves: the workgroup's query rows reach LDS by DMA (waves 4-7, which
   // do no slot resolution), one row per head from row kQRow0 on, in the
@@ -124,7 +133,7 @@ struct Cfg {
   // (4 k-steps) and each group's sum scaled in fp32, so a channel split
   // follows the groups: half 0 takes groups 0-1 and the two rope k-steps,
   // half 1 groups 2-3 and two k-steps of zero Q (10 each).
-  static constexpr int KSQ = QS ? (F8R ? 9 : KVF ? 10 : KS / 2) : KS;
+  static constexpr int KSQ = QS && !KSP ? (F8R ? 9 : KVF ? 10 : KS / 2) : KS;
   static constexpr int NLG = QS ? 2 : 4;                    // fp8: scale groups per wave
   static constexpr int GT = WK * 64;                        // threads per key-group
   static constexpr int NI = F8R ? kF8Slot / 64 : TR * CH / 64;   // DMA instructions per step
@@ -145,6 +154,7 @@ struct Cfg {
   static_assert(F8R || KW * NST * SLOT <= kRingRows * kChunksMax, "ring fits");
   static_assert(F8R || !QS || (KS % 2 == 0 && NW * 64 * MT * 4 * 4 <= (kLdsRows - kRingRows) * kChunksMax * 16),
                 "S exchange fits above the ring");
+  static_assert(!KSP || kXsChunk + 2 * NW * 96 <= kLdsRows * kChunksMax, "key-split P exchange fits above the ring");
   // the last key-group's first fill (slots 0 .. NST - 2) ends at or before the query rows
   static_assert(!QL || (NW == 8 && (KW - 1) * NST * SLOT + (NST - 1) * SLOT <= kQChunk),
                 "query rows clear of the first fill");
@@ -176,7 +186,7 @@ struct Fwd {
   // QK^T k-steps: this wave's first one, and the one its local k-step ks
   // computes (fp8 channel halves: local k-steps 8 and 9 are the rope k-steps
   // 16 and 17, with zero Q in half 1)
-  __device__ __forceinline__ int kbase() const { return C::QS ? (KVF ? cs * 8 : cs * C::KSQ) : 0; }
+  __device__ __forceinline__ int kbase() const { return C::QS && !C::KSP ? (KVF ? cs * 8 : cs * C::KSQ) : 0; }
   // (fp8-resident: channel half cs takes latent groups 2 cs, 2 cs + 1 and
   // rope k-step 16 + cs, nine k-steps each)
   __device__ __forceinline__ int kglob(int ks) const {
@@ -1087,6 +1097,235 @@ struct Fwd {
     }
   }
 
+  // -- key-split 8-wave loop (KSP: 64-head workgroups, one key-group) -------
+  // Wave (hw, cs) computes S^T for keys 16 cs .. 16 cs + 15 of a step against
+  // head tile hw over all D channels (two chains, even / odd k-steps), the
+  // softmax of those 16 keys, and P.V over all 32 keys for its channel half,
+  // with the other 16 keys' P from its partner (same heads, other half)
+  // through LDS. Iteration it, after one workgroup barrier: read the
+  // partner's P of step it and its reference max, QK^T of step it + 1, join
+  // the two references and round both halves' P to the query dtype, the
+  // softmax of step it + 1, P.V of step it, and write P of step it + 1. The
+  // ring and its DMA schedule are run_pipe8's; the last step's P.V follows
+  // the loop. (This pair split replaces the channel-split loop's exchange of
+  // S halves, 6 KB per wave and step, by 1.25 KB of P, and halves each
+  // wave's softmax; each wave reads K for all D channels of its 16 keys.)
+  //
+  // The pair starts from one reference: the max over both halves of step 0
+  // (exchanged once, before the loop), as the channel-split loop's first
+  // step sets it. Later each wave runs the lazy rescale over its own keys
+  // (its reference moves to its own max when one of its keys rises more
+  // than 2^8 above the common one, r0); the pair then joins at the
+  // exchange: if either moved, both take, head by head, the max of r0 and
+  // both halves' maxima of the step, which is where the channel-split loop
+  // moves the reference, and O, l and each P are scaled by 2^(its
+  // reference - the joined one). P is exchanged in fp32 and rounded only
+  // after the join, once, so every P equals exp2(s - reference) as in the
+  // channel-split loop, up to fp32 rounding.
+  static constexpr bool kPipe8K = C::KSP && C::KW == 1 && C::NST == 3;
+  __device__ __forceinline__ int partner() const { return (1 - cs) * HW + hw; }
+  // P in fp32 (this lane's keys 4g .. 4g + 3 of its key half, head c16),
+  // the reference it was computed against and the half's max of the step
+  __device__ __forceinline__ f32x4* kx_p(int b) const {
+    return reinterpret_cast<f32x4*>(lds_ring + C::kXsChunk) + b * (NW * 96);
+  }
+  __device__ __forceinline__ void kx_write(int b, const f32x4& pf, float mloc) const {
+    f32x4* xs = kx_p(b);
+    xs[(cs * HW + hw) * 64 + lane] = pf;
+    reinterpret_cast<float2*>(xs + NW * 64)[(cs * HW + hw) * 64 + lane] = make_float2(m_run, mloc);
+  }
+  __device__ __forceinline__ void kx_read(int b, f32x4& pp, float2& mp) const {
+    const f32x4* xs = kx_p(b);
+    pp = xs[partner() * 64 + lane];
+    mp = reinterpret_cast<const float2*>(xs + NW * 64)[partner() * 64 + lane];
+  }
+  // 2^(a - b) for a <= b (0 for a = -inf)
+  static __device__ __forceinline__ float ref_factor(float a, float b) {
+    return a == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(a - b);
+  }
+  // the P.V operand of step it: own P (po, half max mo) and the partner's
+  // (pp; its reference and half max in mp) on one reference, rounded to the
+  // query dtype; r0 is the pair's reference before step it's softmax. O and
+  // l follow the reference when it moves.
+  __device__ __forceinline__ void kx_join(f32x4 pp, float2 mp, f32x4 po, float mo, float r0, uint32_t (&pk)[4]) {
+    if (__ballot(m_run != r0 || mp.x != r0)) {   // rare: a lazy move in either half
+      const float M = fmaxf(r0, fmaxf(mo, mp.y));
+      const float a = m_run < M ? ref_factor(m_run, M) : 1.f;
+      const float b = mp.x < M ? ref_factor(mp.x, M) : 1.f;
+      // in place (as inline asm): scaled copies of acc made the compiler
+      // copy all of acc on the path that does not scale it
+#pragma unroll
+      for (int i = 0; i < C::NTL; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(acc[i][j]) : "v"(a));
+      l_run *= a;
+      po *= a;
+      pp *= b;
+      m_run = M;
+    }
+    // key tile 0 is half 0's keys, tile 1 half 1's
+    const f32x4 p0 = cs == 0 ? po : pp, p1 = cs == 0 ? pp : po;
+    pk[0] = pack2<QT>(p0[0], p0[1]);
+    pk[1] = pack2<QT>(p0[2], p0[3]);
+    pk[2] = pack2<QT>(p1[0], p1[1]);
+    pk[3] = pack2<QT>(p1[2], p1[3]);
+  }
+  template <typename DmaFn>
+  __device__ __forceinline__ void qk_ks(int sl, f32x4& se, f32x4& so, DmaFn&& dma) {
+    constexpr int SG = kSwzGroup<C::CH>, KPG = SG / 4, KS = C::KS;
+    const int ksw = swz<C::CH>(c16);   // rows c16 and 16 + c16 share the swizzle
+    const uint4* krow = &lds_ring[sl + (cs * 16 + c16) * C::CH];
+    int qo[KPG];
+#pragma unroll
+    for (int j = 0; j < KPG; ++j) qo[j] = (4 * j + g) ^ ksw;
+    auto kfrag = [&](int ks) { return krow[(ks / KPG) * SG + qo[ks % KPG]]; };
+    se = f32x4{0.f, 0.f, 0.f, 0.f};
+    so = se;
+    constexpr int kPfK = C::PFK;
+    uint4 af[kPfK];
+#pragma unroll
+    for (int i = 0; i < kPfK; ++i) af[i] = kfrag(i);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const uint4 a = af[ks % kPfK];
+      if (ks + kPfK < KS) af[ks % kPfK] = kfrag(ks + kPfK);
+      if (ks & 1) so = mfma32k<QT>(a, qf[0][ks], so);
+      else se = mfma32k<QT>(a, qf[0][ks], se);
+      if ((ks & 1) && ks / 2 < C::OPS) dma(ks / 2);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, kPfK, 0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (ks + kPfK < KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int o = KS / 2; o < C::OPS; ++o) dma(o);
+  }
+  // softmax of this wave's 16 keys of a step (S^T = se + so): e = 0 the
+  // mask, max and reference move (returns through resc / alpha whether O
+  // must be scaled after the P.V in flight), e = 1..4 the exps (P in fp32,
+  // pf), 5 the sum
+  static constexpr int kKsB = 6;
+  __device__ __forceinline__ void ks_smax(int e, const f32x4& se, const f32x4& so, int step, f32x4& pf,
+                                          float& mloc, float& lsum, bool& resc, float& alpha) {
+    if (e == 0) {
+      const int nk = min(C::TR, nrows - step * C::TR) - cs * 16;   // my valid keys (may be <= 0)
+      mloc = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float x = g * 4 + j < nk ? (se[j] + so[j]) * p.scale_log2 : -INFINITY;
+        pf[j] = x;
+        mloc = fmaxf(mloc, x);
+      }
+      mloc = rows_max(mloc);
+      resc = __ballot(mloc > m_run + kLazyLog2) != 0;
+      const float m_new = resc ? fmaxf(m_run, mloc) : m_run;
+      alpha = resc ? ref_factor(m_run, m_new) : 1.f;
+      l_run *= alpha;
+      m_run = m_new;
+    } else if (e <= 4) {
+      // (with m_run = -inf every key of this half so far is masked: P = 0)
+      const float x = __builtin_amdgcn_exp2f(pf[e - 1] - fmaxf(m_run, -3.0e38f));
+      pf[e - 1] = x;
+      lsum = e == 1 ? x : lsum + x;
+    } else {
+      l_run += rows_sum(lsum);
+    }
+  }
+  template <int J>
+  __device__ __forceinline__ void pipe8k_j(int it0, f32x4& pown, float& mown, float& r0) {
+    const int it = it0 + J;
+    if (it >= nsteps - 1) return;   // uniform: one key-group; the last step follows the loop
+    constexpr int Jn = (J + 1) % 3, Jf = (J + 2) % 3;
+    // my DMA of step it + 1 has landed; after the barrier every wave's has,
+    // every P of step it is written, and slot Jf is free (as in pipe8_j)
+    wait_vm<0>();
+    lds_barrier();
+    f32x4 pp;
+    float2 mp;
+    kx_read(it & 1, pp, mp);
+    // The DMA goes out unconditionally: in the loop's last iteration it
+    // re-reads step nsteps (rows within the padded row list) into slot Jf,
+    // which no step reads; the wait after the loop drains it.
+    Dma d;
+    prep(d, Jf, min(it + 2, nsteps));
+    f32x4 se, so;
+    qk_ks(slot(Jn), se, so, [&](int o) { fire(d, o); });
+    uint32_t pk[4];
+    kx_join(pp, mp, pown, mown, r0, pk);
+    float lsum = 0.f, alpha = 1.f;
+    bool resc = false;
+    r0 = m_run;
+#pragma unroll
+    for (int e = 0; e < kKsB; ++e) ks_smax(e, se, so, it + 1, pown, mown, lsum, resc, alpha);
+    pv(slot(J), pk, [](int) {});
+    if (resc) {
+#pragma unroll
+      for (int i = 0; i < C::NTL; ++i) acc[i] *= alpha;
+    }
+    kx_write((it + 1) & 1, pown, mown);
+  }
+  __device__ __forceinline__ void run_pipe8k() {
+    if (nsteps > 0) {   // uniform over the workgroup
+      issue(0, 0);
+      if (nsteps > 1) issue(1, 1);
+      wait_steps(nsteps > 1 ? 1 : 0);   // my part of step 0
+      lds_barrier();
+      f32x4 se, so;
+      qk_ks(slot(0), se, so, [](int) {});
+      {
+        // the pair's common first reference: the lazy move over both halves
+        // of step 0 (the softmax below then finds no key above it)
+        const int nk = min(C::TR, nrows) - cs * 16;
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (g * 4 + j < nk) mloc = fmaxf(mloc, (se[j] + so[j]) * p.scale_log2);
+        mloc = rows_max(mloc);
+        if (g == 0) lds_ml[cs * HW + hw][0][c16] = mloc;
+        lds_barrier();
+        mloc = fmaxf(mloc, lds_ml[partner()][0][c16]);
+        if (__ballot(mloc > m_run + kLazyLog2)) {
+          const float m_new = fmaxf(m_run, mloc);
+          l_run *= ref_factor(m_run, m_new);
+          m_run = m_new;
+        }
+      }
+      f32x4 pown;
+      float mown, r0 = m_run;
+      {
+        float lsum = 0.f, alpha = 1.f;
+        bool resc = false;
+#pragma unroll
+        for (int e = 0; e < kKsB; ++e) ks_smax(e, se, so, 0, pown, mown, lsum, resc, alpha);
+        // (O is still zero: nothing to rescale)
+      }
+      kx_write(0, pown, mown);
+      for (int it0 = 0; it0 < nsteps - 1; it0 += 3) {
+        pipe8k_j<0>(it0, pown, mown, r0);
+        pipe8k_j<1>(it0, pown, mown, r0);
+        pipe8k_j<2>(it0, pown, mown, r0);
+      }
+      // the last step: its P exchange and P.V only (the wait also drains
+      // the loop's re-read of step nsteps before the ring is reused)
+      const int it = nsteps - 1;
+      wait_vm<0>();
+      lds_barrier();
+      f32x4 pp;
+      float2 mp;
+      kx_read(it & 1, pp, mp);
+      uint32_t pk[4];
+      kx_join(pp, mp, pown, mown, r0, pk);
+      pv(slot(it % 3), pk, [](int) {});
+    }
+    // the pair's references agree here (joined at the last step); l is the
+    // sum of both halves' sums
+    if (g == 0) lds_ml[cs * HW + hw][1][c16] = l_run;
+    lds_barrier();
+    l_run += lds_ml[partner()][1][c16];
+  }
+
   __device__ __forceinline__ void run() {
     if constexpr (kPipe) {
       run_pipe();
@@ -1094,6 +1333,10 @@ struct Fwd {
     }
     if constexpr (kPipe8) {
       run_pipe8();
+      return;
+    }
+    if constexpr (kPipe8K) {
+      run_pipe8k();
       return;
     }
     if constexpr (KVF != 1) {
@@ -1444,6 +1687,7 @@ sas_fwd_kernel(const FwdParams p) {
   }
   f.m_run = seed_sink ? sink * kLog2e : -INFINITY;
   f.l_run = seed_sink ? 1.f : 0.f;
+  if constexpr (C::KSP) f.l_run = seed_sink && f.cs == 0 ? 1.f : 0.f;   // the sink's term: half 0's sum
 #pragma unroll
   for (int i = 0; i < C::NTL; ++i) f.acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 

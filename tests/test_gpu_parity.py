@@ -474,14 +474,20 @@ def test_swa_exact_and_streaming_schedules_agree():
     assert e_ex <= e_st
 
 
+@pytest.mark.parametrize("win", [127, 135, 143], ids=["at_key0", "at_key8", "at_key16"])
 @pytest.mark.parametrize("K", [16, 300], ids=["jump_in_last_step", "jump_mid_stream"])
-def test_prefill_score_jump_moves_the_reference(K):
+def test_prefill_score_jump_moves_the_reference(K, win):
     """64-head single-split prefill whose top-k rows score ~60 nats (~87 log2
     units) above the window rows: the head max jumps far past the reference
     the first steps set (with K = 16 in the last step, with K = 300 in a
     middle one), so O and l are rescaled by ~2^-87 in one step. Both
-    wave layouts meet the tolerance against the fp64 oracle."""
-    inp = _small(B=1, H=64, q_lens=[300], kv_lens=[1500], K=K, seed=11)
+    wave layouts meet the tolerance against the fp64 oracle. The window
+    (win + 1 rows ahead of the top-k rows) puts the first jumping key at
+    position 0, 8 or 16 of its 32-row step: in the 8-wave kernel, whose wave
+    pairs split a step's keys 0-15 / 16-31, the jump then lands in the first
+    half, in both, or in the second half alone (the halves' references move
+    apart and are joined)."""
+    inp = _small(B=1, H=64, q_lens=[300], kv_lens=[1500], K=K, seed=11, win=win)
     inp.q[:, :, 0] = 40.0
     inp.ori_kv[..., 0] = 0.0
     inp.cmp_kv[..., 0] = 36.0
