@@ -1108,7 +1108,7 @@ struct Fwd {
   // softmax of step it + 1, P.V of step it, and write P of step it + 1. The
   // ring and its DMA schedule are run_pipe8's; the last step's P.V follows
   // the loop. (This pair split replaces the channel-split loop's exchange of
-  // S halves, 6 KB per wave and step, by 1.25 KB of P, and halves each
+  // S halves, 6 KB per wave and step, by 1.5 KB of P, and halves each
   // wave's softmax; each wave reads K for all D channels of its 16 keys.)
   //
   // The pair starts from one reference: the max over both halves of step 0
