@@ -533,6 +533,35 @@ def _fuzz_case(i):
     return kw, splits
 
 
+def _key_split_case(i):
+    """Seeded configuration i for the 64-head 8-wave plan (wave pairs that
+    split each 32-row step's keys): 64 or 128 heads, D 512 or 576, bf16 or
+    fp16, row counts from a few keys (the second key half of the only step
+    empty) to several steps with a ragged last one, 1 to 3 splits."""
+    r = np.random.default_rng(5000 + i)
+    scenario = int(r.choice([1, 2, 3]))
+    B = int(r.integers(1, 4))
+    kw = dict(B=B, H=int(r.choice([64, 128])), q_lens=[int(r.integers(1, 6)) for _ in range(B)],
+              kv_lens=[int(r.choice([int(r.integers(1, 48)), int(r.integers(48, 3001))])) for _ in range(B)],
+              K=int(r.choice([7, 16, 40, 300])) if scenario == 3 else 0, ratio=int(r.choice([4, 8])),
+              bs=int(r.choice([16, 64])), D=int(r.choice([512, 576])), scenario=scenario,
+              dtype=torch.float16 if r.random() < 0.5 else torch.bfloat16,
+              win=int(r.choice([0, 5, 15, 16, 31, 127])), seed=i)
+    return kw, int(r.choice([1, 2, 3]))
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_key_split_pairs_against_oracle(i):
+    """The 64-head 8-wave kernel (forced) on seeded small configurations:
+    out within atol = rtol = 2e-2, LSE within 1e-3 of the oracle."""
+    kw, splits = _key_split_case(i)
+    print(f"[key-split {i}] {kw} splits={splits}", flush=True)
+    inp = _small(**kw)
+    out, lse, ns = _run(inp, num_splits=splits, head_waves=4, waves=8)
+    ref_out, ref_lse = _oracle(inp)
+    _check_baseline(out, lse, ref_out, ref_lse, f"key-split {i} (splits {ns})")
+
+
 @pytest.mark.parametrize("i", range(64))
 def test_random_configurations_against_oracle(i):
     """Random configurations (seeded) through the planner's own choices or an
