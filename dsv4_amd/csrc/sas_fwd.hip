@@ -1081,10 +1081,12 @@ struct Fwd {
     pv(slot(J), pk, [](int) {});
   }
 
-  __device__ __forceinline__ void run_pipe8() {
+  template <typename QFn>
+  __device__ __forceinline__ void run_pipe8(QFn&& qload) {
     if (nsteps <= 0) return;   // uniform over the workgroup
     issue(0, 0);
     if (nsteps > 1) issue(1, 1);
+    qload();
     wait_steps(nsteps > 1 ? 1 : 0);   // my part of step 0
     lds_barrier();
     f32x4 s0[C::MT], so[C::MT];
@@ -1266,10 +1268,12 @@ struct Fwd {
     }
     kx_write((it + 1) & 1, pown, mown);
   }
-  __device__ __forceinline__ void run_pipe8k() {
+  template <typename QFn>
+  __device__ __forceinline__ void run_pipe8k(QFn&& qload) {
     if (nsteps > 0) {   // uniform over the workgroup
       issue(0, 0);
       if (nsteps > 1) issue(1, 1);
+      qload();
       wait_steps(nsteps > 1 ? 1 : 0);   // my part of step 0
       lds_barrier();
       f32x4 se, so;
@@ -1326,17 +1330,22 @@ struct Fwd {
     l_run += lds_ml[partner()][1][c16];
   }
 
-  __device__ __forceinline__ void run() {
+  // qload(): the wave's Q^T fragments from the LDS query rows (8-wave
+  // kernels), run after the first steps' row DMA is issued (the rows lie
+  // outside its slots), so the query reads overlap the rows' round trip
+  // instead of delaying its issue
+  template <typename QFn>
+  __device__ __forceinline__ void run(QFn&& qload) {
     if constexpr (kPipe) {
       run_pipe();
       return;
     }
     if constexpr (kPipe8) {
-      run_pipe8();
+      run_pipe8(qload);
       return;
     }
     if constexpr (kPipe8K) {
-      run_pipe8k();
+      run_pipe8k(qload);
       return;
     }
     if constexpr (KVF != 1) {
@@ -1347,6 +1356,7 @@ struct Fwd {
       if (nsteps > 0) { fload(0); fstore(0); }
       if (nsteps > 1) fload(1);
     }
+    qload();
     for (int it0 = 0; it0 < nsteps_max; it0 += C::NST) {
       step_j<0>(it0);
       step_j<1>(it0);
@@ -1681,10 +1691,7 @@ sas_fwd_kernel(const FwdParams p) {
   const bool seed_sink = p.nsplit == 1 && f.kw == 0;
   const float sink = (seed_sink || EXW) ? p.sinks[hq] : 0.f;
   __builtin_amdgcn_s_waitcnt(0);
-  if constexpr (C::QL) {
-    __syncthreads();   // every wave's query DMA has landed
-    f.q_from_lds();    // read before the first step barrier, ahead of any write to these rows
-  }
+  if constexpr (C::QL) __syncthreads();   // every wave's query DMA has landed
   f.m_run = seed_sink ? sink * kLog2e : -INFINITY;
   f.l_run = seed_sink ? 1.f : 0.f;
   if constexpr (C::KSP) f.l_run = seed_sink && f.cs == 0 ? 1.f : 0.f;   // the sink's term: half 0's sum
@@ -1692,7 +1699,9 @@ sas_fwd_kernel(const FwdParams p) {
   for (int i = 0; i < C::NTL; ++i) f.acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if constexpr (EXW) f.run_exact(wave, p.nsplit == 1 ? sink * kLog2e : -INFINITY);
-  else f.run();
+  // (the query rows are read before the first step barrier, ahead of any
+  // write to them)
+  else f.run([&] { if constexpr (C::QL) f.q_from_lds(); });
   epilogue<HW, NW, C::CS, QT>(p, k, tid, wave, lane, f.m_run, f.l_run, f.acc);
 }
 
