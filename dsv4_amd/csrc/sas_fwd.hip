@@ -1988,10 +1988,15 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
     // merge (32-token, 64-head decode: 18.4 µs at 32 heads x 4 splits,
     // 21.1 µs at 64 heads x 8 splits); else 64-head groups, which leave room
     // for twice the splits (31-token, 128-head decode: 28.7 µs at 64 x 4
-    // against 32.4 µs at 32 x 2). fp8 rows alike (8-token, 128-head fp8
-    // decode: 23.2 µs at 32 heads x 8 waves x 8 splits, 26.3 µs at 64 heads
-    // x 4 waves x 12 splits).
-    if (a->H % 64 == 0 && T * (a->H / 64) >= 2 * cus) hw = 4;
+    // against 32.4 µs at 32 x 2). fp8 rows take 32-head groups whenever the
+    // heads allow: their 8-wave kernel keeps the rows fp8 in LDS, while the
+    // 64-head fp8 kernels (4 waves, rows converted through registers) spill
+    // (8-token, 128-head fp8 decode: 23.2 µs at 32 heads x 8 waves x 8
+    // splits, 26.3 µs at 64 heads x 4 waves x 12 splits; 31-token, 128-head
+    // fp8 decode 30.3 against 42.2 µs; 4K-token, 64-head fp8 prefill 686
+    // against 880 µs).
+    if (fp8 && a->H % 32 == 0) hw = 2;
+    else if (a->H % 64 == 0 && T * (a->H / 64) >= 2 * cus) hw = 4;
     else if (a->H % 64 == 0 && one_round_splits(2) < 4) hw = 4;
     else if (a->H % 32 == 0) hw = 2;
     else hw = 1;
