@@ -16,18 +16,24 @@
 //     MFMAs of the step before, into the slot that step freed; one workgroup
 //     barrier per step. Tiles are row-major with an XOR swizzle of 16-byte
 //     chunks that keeps both operand reads below bank-conflict free. fp8 rows
-//     go through registers instead (dequantised to bf16 on the way). With
-//     one wave per key-group the step loop has no workgroup barrier.
+//     reach LDS the same way and stay fp8 there in the 32-head 8-wave plan
+//     (each operand fragment converted to bf16 in registers); the other fp8
+//     plans convert them through registers into bf16 slots. With one wave
+//     per key-group the step loop has no workgroup barrier.
 //  3. Per step and wave:  S^T[TR keys x 16 heads] = K . Q^T  (16x16x32 MFMA,
 //     A from LDS, Q^T resident in VGPRs), sink-seeded online softmax in the
 //     log2 domain, P rounded to the query dtype, then
 //     O^T[channels x 16 heads] += V^T . P^T where the V^T operand comes
 //     straight from the row-major tile with ds_read_b64_tr_b16 and P^T is
 //     already in the register layout the MFMA wants (the S^T accumulator
-//     layout).
+//     layout). With 8 waves the two waves of a 16-head pair split O by
+//     channels and share QK^T: by channels (each sums half of S; 32-head
+//     groups) or by keys (each takes half of the step's keys and hands its
+//     P to the other; 64-head groups).
 //  4. Key-groups merge through LDS (max / sum rescale); the result is the
-//     output + LSE, or with several KV splits an unnormalised fp32 partial
-//     that the LSE combine kernel merges with the sink.
+//     output + LSE, or with several KV splits an unnormalised partial (fp16
+//     scaled by a power of two for bf16 outputs, fp32 for fp16) that the LSE
+//     combine kernel merges with the sink.
 //
 // Semantics follow sparse_attn_sharedkv_tilelang/kernel.py:254-277 (work
 // decode), :628-722 (window / compressed masks), :594-617 (sink seed),
@@ -69,9 +75,10 @@ namespace {
 
 // NW waves = HW head-waves x CS channel-halves x KW key-groups; D = q/k
 // channels; QT = query dtype; KVF: 0 = cache rows in the query dtype,
-// 1 = 656-byte fp8 rows. With 8 waves (2 per SIMD, 256 registers each) a
-// wave holds the O of its 16 heads for half of the 512 V channels (CS = 2):
-// both halves compute the same S = QK^T, each accumulates its own channels.
+// 1 / 2 = 656-byte fp8 rows (converted into bf16 slots / kept fp8 in LDS).
+// With 8 waves (2 per SIMD, 256 registers each) a wave holds the O of its
+// 16 heads for half of the 512 V channels (CS = 2), and the pair shares
+// the QK^T work (by channels, or by keys with KSP).
 template <int HW, int NW, int D, typename QT, int KVF>
 struct Cfg {
   // KVF == 2: fp8 rows stay fp8 in LDS (LDS-DMA like bf16 rows) and each
@@ -84,10 +91,10 @@ struct Cfg {
   static constexpr int WK = HW * CS;                        // waves sharing a key-group's slots
   static constexpr int KW = NW / WK;
   static constexpr int NTL = kDV / 16 / CS;                 // 16-channel O tiles per wave
-  // With two channel halves the QK^T k-steps are split as well: each wave of
-  // a pair sums S over its half of the D channels and the pair adds the two
-  // halves through LDS (no QK^T work is duplicated). The exchange buffer
-  // takes the ring rows above kRingRows.
+  // With two channel halves the QK^T k-steps are split as well (but see KSP
+  // below): each wave of a pair sums S over its half of the D channels and
+  // the pair adds the two halves through LDS (no QK^T work is duplicated).
+  // The exchange buffer takes the ring rows above kRingRows.
   static constexpr bool QS = CS == 2;
   // Key-split QK^T (the 64-head, 8-wave, one-key-group plan with
   // SAS_KSPLIT): the two waves of a pair each compute S over all D channels
@@ -1005,7 +1012,8 @@ struct Fwd {
   }
 
   // -- software-pipelined loop of the 8-wave channel-split kernel -----------
-  // (64-head workgroups, one key-group: the prefill configuration.) The two
+  // (64-head workgroups, one key-group, built with SAS_KSPLIT=0; the default
+  // for this configuration is the key-split loop, run_pipe8k.) The two
   // waves of a 16-head pair each sum S over half of D and exchange their
   // halves through LDS. Iteration it, after one workgroup barrier, reads the
   // exchanged S of step it, then runs the QK^T MFMAs of step it + 1 with the
