@@ -2035,6 +2035,19 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
     ns = (int)std::min<long long>(one_round_splits(hw), max_by_len);
   }
   ns = std::max(1, std::min(ns, a->num_splits > 0 ? kMaxSplits : kMaxAutoSplits));
+  // fp8 rows in the 32-head 8-wave plan: two key-groups of 32-row steps per
+  // workgroup. Of the split counts whose workgroups take the same number of
+  // steps (the key-group holding the first share of rows sets the time),
+  // the fewest: fewer partials to write and merge (C5, 1152 slots: 8 splits
+  // give key-groups of 96 + 48 rows, 6 splits 96 + 96; 22.6-22.8 against
+  // 23.0 µs with caches flushed, 18.0 against 18.3-18.4 µs warm)
+  if (a->num_splits <= 0 && fp8 && hw == 2 && nw == 8 && !pl->exact) {
+    auto steps = [&](int n) {
+      const int r = (pl->nslots + n - 1) / n;
+      return (r + 63) / 64;   // 32-row steps of the first key-group's ceil(r / 64) x 32 rows
+    };
+    while (ns > 1 && steps(ns - 1) == steps(ns)) --ns;
+  }
   // 16-head groups run the exact schedule when a split's rows fit the ring
   // (every row gathered at once, no per-step barriers; 1-token, 16-head
   // decode: 12.7 µs against 15.5 µs for the register-streaming decode
