@@ -1000,7 +1000,8 @@ extern "C" int sas_bwd_v1(const SasBwdArgs* ba, void* stream) {
   bp.d_ori = ba->d_ori_kv;
   bp.d_cmp = ba->d_cmp_kv;
   bp.d_sinks = ba->d_sinks;
-  const long long nblocks_ll = (long long)((a->T + kXcds - 1) / kXcds) * fp.nhg * fp.nsplit * kXcds;
+  fp.nxcd = device_xcds();
+  const long long nblocks_ll = (long long)((a->T + fp.nxcd - 1) / fp.nxcd) * fp.nhg * fp.nsplit * fp.nxcd;
   if (nblocks_ll > INT_MAX) return set_error(SAS_EINVAL, "bwd: %lld workgroups beyond one launch", nblocks_ll);
   const int nblocks = (int)nblocks_ll;
   // The key-major window pass (sas_bwd_win_kernel): by default when query

@@ -1932,8 +1932,9 @@ sas_combine_kernel(const FwdParams p) {
   // token t's workgroups go to the XCD its split workgroups ran on
   // (item_index's dealing), whose L2 still holds the partials they wrote
   // (measured: C2 call 24.3 -> 23.7 µs)
-  const int x = (int)(blockIdx.x % kXcds), l = (int)(blockIdx.x / kXcds);
-  const int t = p.T - 1 - ((l / nhb) * kXcds + x);
+  const unsigned nx = (unsigned)p.nxcd;
+  const int x = (int)(blockIdx.x % nx), l = (int)(blockIdx.x / nx);
+  const int t = p.T - 1 - ((l / nhb) * p.nxcd + x);
   if (t < 0) return;
   const int h0 = (l % nhb) * kHeads;
   merge_partials<QT>(p, t, h0, min(kHeads, p.H - h0), threadIdx.x, kCombineThreads);
@@ -1978,14 +1979,15 @@ int make_plan(const SasFwdArgs* a, Plan* pl) {
   pl->exact = a->scenario == SAS_SWA && pl->nslots <= kLdsRows && ns <= 1 && (a->waves == 0 || a->waves == 4);
   const bool fp8 = a->kv_dtype == SAS_DT_FP8_E4M3_ROW656;
   // Every workgroup of a token runs on the token's XCD (item_index deals
-  // tokens round-robin over the XCDs, blockIdx % 8): with one workgroup per
-  // CU, a grid fills the chip in one round when each XCD's share,
-  // ceil(T / 8) tokens x head groups x splits, fits its CUs. A second round
+  // tokens round-robin over the XCDs, blockIdx % XCDs): with one workgroup
+  // per CU, a grid fills the chip in one round when each XCD's share,
+  // ceil(T / XCDs) tokens x head groups x splits, fits its CUs. A second round
   // roughly doubles a decode call (31-token, 128-head decode with 5 splits
   // of 64 heads: 43.8 µs, 4 splits: 28.7 µs).
   const int cus = sas::device_cus();
-  const long long cus_x = std::max(1, cus / kXcds);
-  const long long tpx = (T + kXcds - 1) / kXcds;
+  const int xcds = sas::device_xcds();
+  const long long cus_x = std::max(1, cus / xcds);
+  const long long tpx = (T + xcds - 1) / xcds;
   auto one_round_splits = [&](int h) { return std::max<long long>(1, cus_x / (tpx * (a->H / (16 * h)))); };
   if (hw <= 0) {
     // Heads sharing one gathered tile inside a workgroup (16 per wave); each
@@ -2111,7 +2113,8 @@ int dispatch_hw(int hw, int nw, bool exact, const FwdParams& fp, int nb, hipStre
 
 int launch_combine(const FwdParams& fp, int out_dtype, hipStream_t st) {
   constexpr int kHeads = kCombineThreads / (kDV / kCombineCpt);
-  const dim3 grid((unsigned)(((fp.T + kXcds - 1) / kXcds) * kXcds * ((fp.H + kHeads - 1) / kHeads)));
+  const long long nx = fp.nxcd;
+  const dim3 grid((unsigned)(((fp.T + nx - 1) / nx) * nx * ((fp.H + kHeads - 1) / kHeads)));
   if (out_dtype == SAS_DT_BF16)
     hipLaunchKernelGGL(sas_combine_kernel<__bf16>, grid, dim3(kCombineThreads), 0, st, fp);
   else if (out_dtype == SAS_DT_FP16)
@@ -2136,6 +2139,7 @@ int combine_impl(const SasCombineArgs* a, hipStream_t st) {
   fp.out = (uint8_t*)a->out;
   fp.lse = a->lse;
   fp.T = (int)a->T; fp.H = (int)a->H; fp.nsplit = (int)a->S;
+  fp.nxcd = sas::device_xcds();
   return launch_combine(fp, a->out_dtype, st);
 }
 
@@ -2205,8 +2209,9 @@ extern "C" int sas_fwd_v1(const SasFwdArgs* a, void* stream) {
   fp.cmp_ratio = std::max(1, a->cmp_ratio); fp.win_left = a->win_left;
   fp.scale_log2 = a->softmax_scale * kLog2e;
   fp.nsplit = pl.nsplit; fp.slots_per_split = pl.sps; fp.nhg = pl.nhg;
-  // item_index(): ceil(T / 8) tokens per XCD, nhg * nsplit workgroups each
-  const long long nblocks_ll = (long long)((a->T + kXcds - 1) / kXcds) * pl.nhg * pl.nsplit * kXcds;
+  // item_index(): ceil(T / XCDs) tokens per XCD, nhg * nsplit workgroups each
+  fp.nxcd = sas::device_xcds();
+  const long long nblocks_ll = (long long)((a->T + fp.nxcd - 1) / fp.nxcd) * pl.nhg * pl.nsplit * fp.nxcd;
   if (nblocks_ll > INT_MAX)
     return sas::set_error(SAS_EINVAL, "%lld workgroups (tokens x head groups x splits) beyond one launch",
                           nblocks_ll);

@@ -24,7 +24,6 @@ constexpr int kDV = 512;          // output / V channels
 constexpr int kMaxSlots = 1280;   // slot range one workgroup may own
 constexpr int kRoundsMax = kMaxSlots / 256;  // slot rounds at 256 threads
 constexpr int kMaxWaves = 8;
-constexpr int kXcds = 8;          // MI355X: 8 XCDs, workgroups dealt round-robin
 constexpr int kRow656 = 656;      // fp8 cache row bytes
 constexpr int kChunksMax = 72;    // 16-byte chunks of a 576-channel bf16 row
 constexpr int kLdsRows = 128;     // rows of ring storage per workgroup
@@ -46,6 +45,29 @@ inline int device_cus() {
   int n = cached[dev].load(std::memory_order_relaxed);
   if (n > 0) return n;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return kDefault;
+  }
+  cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// XCDs of the current device: a launch deals its workgroups to them
+// round-robin (workgroup b runs on XCD b % XCDs), and the grids place each
+// token's workgroups on one XCD by that rule. Queried once per device; 8
+// (MI355X) when no device answers. The count only places work: any value
+// gives the same results.
+inline int device_xcds() {
+  constexpr int kMaxDev = 64, kDefault = 8;
+  static std::atomic<int> cached[kMaxDev] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+    (void)hipGetLastError();
+    return kDefault;
+  }
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || n <= 0 || n > 64) {
     (void)hipGetLastError();
     return kDefault;
   }
@@ -105,6 +127,7 @@ struct FwdParams {
   int K, scenario, cmp_ratio, win_left;
   float scale_log2;
   int nsplit, slots_per_split, nhg;
+  int nxcd;      // XCDs the grid is dealt over (device_xcds())
   int part_nt;   // 1: split partials go out with non-temporal stores
   int out_nt;    // 1: the output (one split) goes out with non-temporal stores
 };
@@ -346,15 +369,16 @@ struct Tok {
 };
 
 // Work item of this workgroup, or -1 for a padding workgroup. Tokens are
-// dealt round-robin to the 8 XCDs (blockIdx % 8 is the XCD), latest token
-// first; all head groups and splits of a token go to one XCD and share its
+// dealt round-robin to the device's XCDs (blockIdx % nxcd is the XCD), latest
+// token first; all head groups and splits of a token go to one XCD and share its
 // L2. Every XCD then gets the same mix of long and short token rows (causal
 // prefill: rows grow with the position), and the longest items start first.
 __device__ __forceinline__ int item_index(const FwdParams& p) {
-  const int x = (int)(blockIdx.x % kXcds), l = (int)(blockIdx.x / kXcds);
+  const unsigned nx = (unsigned)p.nxcd;
+  const int x = (int)(blockIdx.x % nx), l = (int)(blockIdx.x / nx);
   const int per_tok = p.nhg * p.nsplit;
   const int q = l / per_tok, sub = l - q * per_tok;
-  const int t = p.T - 1 - (q * kXcds + x);
+  const int t = p.T - 1 - (q * p.nxcd + x);
   return t >= 0 ? t * per_tok + sub : -1;
 }
 
